@@ -1,0 +1,255 @@
+// extern "C" boundary of libomo_mxfp4.so: argument validation, then launch.
+// Declarations and the reference interface each entry point replaces are in
+// include/omo_mxfp4.h. No function here allocates device memory or
+// synchronizes; every check runs on the host before any HIP call.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/omo_mxfp4.h"
+#include "omo_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return OMO_OK;
+}
+
+int from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(OMO_ERR_HIP, "%s: HIP launch failed: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+#define REQUIRE(cond, ...)                                  \
+  do {                                                      \
+    if (!(cond)) return fail(OMO_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+// A buffer that must hold `need` units: non-null when need > 0, large enough.
+#define REQUIRE_BUF(name, ptr, have, need)                                                            \
+  do {                                                                                                \
+    REQUIRE((have) >= 0 && (need) >= 0, "%s: negative size", name);                                   \
+    REQUIRE((need) == 0 || (ptr) != nullptr, "%s: null pointer", name);                               \
+    REQUIRE((have) >= (need), "%s: buffer holds %lld, needs %lld", name, (long long)(have), (long long)(need)); \
+  } while (0)
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Shared checks of the three requant entry points taking (rows, row_bytes).
+int check_requant_common(const char* fn, const void* input, int64_t rows, int64_t row_bytes, int scale_ue8m0) {
+  REQUIRE(rows >= 0 && row_bytes >= 0, "%s: negative shape", fn);
+  if (scale_ue8m0) return fail(OMO_ERR_UNSUPPORTED, "%s: scale_ue8m0 is not supported (the reference asserts it off)", fn);
+  REQUIRE(rows * row_bytes % 128 == 0, "%s: input.numel() %% 128 != 0 (input.numel()=%lld)", fn,
+          (long long)(rows * row_bytes));
+  (void)input;
+  return OMO_OK;
+}
+
+int requant_rowwise(const char* fn, const void* input, int64_t rows, int64_t row_bytes, const void* input_s,
+                    int64_t input_s_bytes, void* output_q, int64_t output_q_bytes, void* output_s,
+                    int64_t output_s_elems, int scale_ue8m0, void* stream) {
+  int rc = check_requant_common(fn, input, rows, row_bytes, scale_ue8m0);
+  if (rc != OMO_OK) return rc;
+  REQUIRE(row_bytes % 64 == 0, "%s: row bytes must be a multiple of 64 (got %lld); pad as the wrapper does", fn,
+          (long long)row_bytes);
+  const int64_t n = rows * row_bytes;
+  REQUIRE_BUF("input", input, n, n);
+  REQUIRE_BUF("input_s", input_s, input_s_bytes, n / 16);
+  REQUIRE_BUF("output_q", output_q, output_q_bytes, 2 * n);
+  REQUIRE_BUF("output_s", output_s, output_s_elems, n / 64);
+  REQUIRE(n / 64 < (int64_t)1 << 31, "%s: too many 128-element groups", fn);
+  REQUIRE(aligned(input, 4) && aligned(input_s, 4) && aligned(output_q, 8) && aligned(output_s, 4),
+          "%s: misaligned buffer (input/input_s need 4 B, output_q 8 B)", fn);
+  if (n == 0) return ok();
+  return from_hip(omo_hip::launch_mxfp4_to_fp8(input, input_s, output_q, static_cast<float*>(output_s), rows,
+                                               row_bytes, as_stream(stream)),
+                  fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int omo_hip_abi_version(void) { return OMO_ABI_VERSION; }
+
+const char* omo_hip_status_string(int status) {
+  switch (status) {
+    case OMO_OK: return "ok";
+    case OMO_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case OMO_ERR_UNSUPPORTED: return "unsupported";
+    case OMO_ERR_HIP: return "HIP error";
+    default: return "unknown status";
+  }
+}
+
+const char* omo_hip_last_error(void) { return g_err; }
+
+int omo_hip_per_token_group_quant_fp4(const void* input, int64_t numel, void* output_q, int64_t output_q_bytes,
+                                      void* output_s, int64_t output_s_bytes, int group_size, float eps,
+                                      float fp4_min, float fp4_max, int scale_ue8m0, void* stream) {
+  const char* fn = "omo_per_token_group_quant_fp4";
+  REQUIRE(group_size > 0, "%s: group_size must be positive", fn);
+  REQUIRE(numel >= 0 && numel % group_size == 0, "%s: input.numel() %% group_size != 0", fn);
+  if (scale_ue8m0)
+    return fail(OMO_ERR_UNSUPPORTED, "%s: scale_ue8m0 (column-major int32 scales) is not supported", fn);
+  if (group_size != 32)
+    return fail(OMO_ERR_UNSUPPORTED, "%s: group_size must be 32 (MXFP4 blocks), got %d", fn, group_size);
+  REQUIRE(std::isfinite(eps) && std::isfinite(fp4_min) && std::isfinite(fp4_max) && fp4_max > 0.0f,
+          "%s: eps, fp4_min, fp4_max must be finite and fp4_max > 0", fn);
+  REQUIRE_BUF("input", input, numel, numel);
+  REQUIRE_BUF("output_q", output_q, output_q_bytes, numel / 2);
+  REQUIRE_BUF("output_s", output_s, output_s_bytes, numel / 32);
+  REQUIRE(aligned(input, 16) && aligned(output_q, 4), "%s: input must be 16-byte and output_q 4-byte aligned", fn);
+  if (numel == 0) return ok();
+  return from_hip(omo_hip::launch_quant_rowwise(input, output_q, output_s, numel, eps, fp4_min, fp4_max,
+                                                as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_per_token_Mxfp4ToBf16_dequant(const void* input, int64_t input_bytes, const void* input_s,
+                                          int64_t input_s_bytes, void* output_q, int64_t output_q_elems,
+                                          void* output_s, int64_t output_s_bytes, int group_size, float eps,
+                                          float fp4_min, float fp4_max, int scale_ue8m0, void* stream) {
+  const char* fn = "omo_per_token_Mxfp4ToBf16_dequant";
+  (void)output_s; (void)output_s_bytes; (void)group_size; (void)eps; (void)fp4_min; (void)fp4_max;
+  if (scale_ue8m0) return fail(OMO_ERR_UNSUPPORTED, "%s: scale_ue8m0 is not supported (the reference asserts it off)", fn);
+  REQUIRE(input_bytes >= 0 && input_bytes % 128 == 0, "%s: input.numel() %% 128 != 0", fn);
+  REQUIRE_BUF("input", input, input_bytes, input_bytes);
+  REQUIRE_BUF("input_s", input_s, input_s_bytes, input_bytes / 16);
+  REQUIRE_BUF("output_q", output_q, output_q_elems, 2 * input_bytes);
+  REQUIRE(aligned(input, 4) && aligned(output_q, 16), "%s: input must be 4-byte and output_q 16-byte aligned", fn);
+  if (input_bytes == 0) return ok();
+  return from_hip(omo_hip::launch_dequant_bf16(input, input_s, output_q, input_bytes, as_stream(stream)), fn);
+}
+
+int omo_hip_per_token_Mxfp4ToFp8(const void* input, int64_t rows, int64_t row_bytes, const void* input_s,
+                                 int64_t input_s_bytes, void* output_q, int64_t output_q_bytes, void* output_s,
+                                 int64_t output_s_elems, int group_size, float eps, float fp4_min, float fp4_max,
+                                 int scale_ue8m0, void* stream) {
+  (void)group_size; (void)eps; (void)fp4_min; (void)fp4_max;
+  return requant_rowwise("omo_per_token_Mxfp4ToFp8", input, rows, row_bytes, input_s, input_s_bytes, output_q,
+                         output_q_bytes, output_s, output_s_elems, scale_ue8m0, stream);
+}
+
+int omo_hip_per_token_Mxfp4ToBf16ToFp8(const void* input, int64_t rows, int64_t row_bytes, const void* input_s,
+                                       int64_t input_s_bytes, void* output_q, int64_t output_q_bytes, void* output_s,
+                                       int64_t output_s_elems, int group_size, float eps, float fp4_min,
+                                       float fp4_max, int scale_ue8m0, void* stream) {
+  (void)group_size; (void)eps; (void)fp4_min; (void)fp4_max;
+  return requant_rowwise("omo_per_token_Mxfp4ToBf16ToFp8", input, rows, row_bytes, input_s, input_s_bytes, output_q,
+                         output_q_bytes, output_s, output_s_elems, scale_ue8m0, stream);
+}
+
+int omo_hip_per_token_Mxfp4ToFp8_col(const void* input, int64_t rows, int64_t row_bytes, const void* input_s,
+                                     int64_t input_s_bytes, void* output_q, int64_t output_q_bytes, void* output_s,
+                                     int64_t output_s_elems, int group_size, float eps, float fp4_min, float fp4_max,
+                                     int scale_ue8m0, void* stream) {
+  const char* fn = "omo_per_token_Mxfp4ToFp8_col";
+  (void)group_size; (void)fp4_min; (void)fp4_max;
+  int rc = check_requant_common(fn, input, rows, row_bytes, scale_ue8m0);
+  if (rc != OMO_OK) return rc;
+  REQUIRE(rows % 128 == 0 && row_bytes % 128 == 0,
+          "%s: rows and row bytes must be multiples of 128 (got %lld x %lld); the reference reads whole "
+          "128x128-byte tiles without bounds checks", fn, (long long)rows, (long long)row_bytes);
+  REQUIRE(!std::isnan(eps), "%s: eps is NaN", fn);
+  const int64_t n = rows * row_bytes;
+  REQUIRE_BUF("input", input, n, n);
+  REQUIRE_BUF("input_s", input_s, input_s_bytes, n / 16);
+  REQUIRE_BUF("output_q", output_q, output_q_bytes, 2 * n);
+  REQUIRE_BUF("output_s", output_s, output_s_elems, (rows / 128) * 2 * row_bytes);
+  REQUIRE(aligned(input, 16) && aligned(input_s, 8) && aligned(output_q, 16) && aligned(output_s, 4),
+          "%s: input/output_q need 16-byte, input_s 8-byte alignment", fn);
+  if (n == 0) return ok();
+  return from_hip(omo_hip::launch_mxfp4_to_fp8_col(input, input_s, output_q, static_cast<float*>(output_s), rows,
+                                                   row_bytes, eps, as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(const void* input, int64_t rows, int64_t row_bytes, const void* input_s,
+                                             int64_t input_s_rows, int64_t input_s_cols, void* output_q,
+                                             int64_t output_q_rows, int64_t output_q_cols, void* output_s,
+                                             int64_t output_s_rows, int64_t output_s_cols, float eps, void* stream) {
+  const char* fn = "omo_per_token_Mxfp4RowToBf16ToFp8Col";
+  REQUIRE(rows >= 0 && row_bytes >= 0, "%s: negative shape", fn);
+  const int64_t M = rows, N = row_bytes * 2;
+  // the shape checks of per_token_Mxfp4RowToBf16ToFp8Col.cu:219-224
+  REQUIRE(input_s_rows == M, "%s: input_s.size(0) != M", fn);
+  REQUIRE(input_s_cols == (N + 31) / 32, "%s: input_s.size(1) != ceil(N/32)", fn);
+  REQUIRE(output_q_rows == N && output_q_cols == M, "%s: output_q must be [N, M]", fn);
+  REQUIRE(output_s_rows == (M + 127) / 128 && output_s_cols == N, "%s: output_s must be [ceil(M/128), N]", fn);
+  REQUIRE(!std::isnan(eps), "%s: eps is NaN", fn);
+  REQUIRE_BUF("input", input, M * row_bytes, M * row_bytes);
+  REQUIRE_BUF("input_s", input_s, input_s_rows * input_s_cols, M * ((N + 31) / 32));
+  REQUIRE_BUF("output_q", output_q, output_q_rows * output_q_cols, N * M);
+  REQUIRE_BUF("output_s", output_s, output_s_rows * output_s_cols, ((M + 127) / 128) * N);
+  REQUIRE(aligned(output_s, 4), "%s: output_s must be 4-byte aligned", fn);
+  if (M == 0 || N == 0) return ok();
+  return from_hip(omo_hip::launch_row_to_fp8_col(input, input_s, output_q, static_cast<float*>(output_s), M, N, eps,
+                                                 as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(const void* input, int64_t rows, int64_t row_bytes,
+                                                    const void* input_s, int64_t input_s_bytes, void* output_q,
+                                                    int64_t output_q_bytes, void* output_s, int64_t output_s_elems,
+                                                    const int32_t* m_splits, const int32_t* split_offsets,
+                                                    const int32_t* scale_offsets, int64_t num_splits,
+                                                    int64_t max_split_len, float eps, void* stream) {
+  const char* fn = "omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit";
+  REQUIRE(rows >= 0 && row_bytes >= 0 && num_splits >= 0 && max_split_len >= 0, "%s: negative shape", fn);
+  REQUIRE(num_splits <= 65535, "%s: at most 65535 splits", fn);
+  REQUIRE(!std::isnan(eps), "%s: eps is NaN", fn);
+  const int64_t M = rows, N = row_bytes * 2;
+  REQUIRE_BUF("input", input, M * row_bytes, M * row_bytes);
+  // the kernel reads scale byte row*(N/32) + col/32 for rows < M, cols < N
+  const int64_t s_need = M == 0 || N == 0 ? 0 : (M - 1) * (N / 32) + (N - 1) / 32 + 1;
+  REQUIRE_BUF("input_s", input_s, input_s_bytes, s_need);
+  REQUIRE_BUF("output_q", output_q, output_q_bytes, M * N);
+  REQUIRE(output_s_elems >= 0 && (output_s_elems == 0 || output_s != nullptr), "%s: output_s", fn);
+  REQUIRE(num_splits == 0 || (m_splits && split_offsets && scale_offsets), "%s: null split metadata", fn);
+  REQUIRE(aligned(output_s, 4) && aligned(m_splits, 4) && aligned(split_offsets, 4) && aligned(scale_offsets, 4),
+          "%s: misaligned buffer", fn);
+  if (num_splits == 0 || N == 0) return ok();
+  const int64_t out_s_rows = output_s_elems / N;
+  return from_hip(omo_hip::launch_row_to_fp8_col_msplit(input, input_s, output_q, static_cast<float*>(output_s), M, N,
+                                                        m_splits, split_offsets, scale_offsets, num_splits,
+                                                        max_split_len, output_q_bytes, out_s_rows, eps,
+                                                        as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_quant_mxfp4_dual(const void* input, int64_t rows, int64_t cols, void* row_q, int64_t row_q_bytes,
+                             void* row_s, int64_t row_s_bytes, void* col_q, int64_t col_q_bytes, void* col_s,
+                             int64_t col_s_bytes, float eps, void* stream) {
+  const char* fn = "omo_quant_mxfp4_dual";
+  REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", fn);
+  REQUIRE(rows % 32 == 0 && cols % 32 == 0, "%s: rows and cols must be multiples of 32 (got %lld x %lld)", fn,
+          (long long)rows, (long long)cols);
+  REQUIRE(rows / 32 <= 65535, "%s: rows/32 exceeds the grid limit", fn);
+  REQUIRE(std::isfinite(eps), "%s: eps must be finite", fn);
+  const int64_t n = rows * cols;
+  REQUIRE_BUF("input", input, n, n);
+  REQUIRE_BUF("row_q", row_q, row_q_bytes, n / 2);
+  REQUIRE_BUF("row_s", row_s, row_s_bytes, n / 32);
+  REQUIRE_BUF("col_q", col_q, col_q_bytes, n / 2);
+  REQUIRE_BUF("col_s", col_s, col_s_bytes, n / 32);
+  REQUIRE(aligned(input, 16) && aligned(col_q, 16) && aligned(row_q, 4), "%s: misaligned buffer", fn);
+  if (n == 0) return ok();
+  return from_hip(omo_hip::launch_quant_dual(input, row_q, row_s, col_q, col_s, rows, cols, eps, as_stream(stream)),
+                  fn);
+}
+
+}  // extern "C"

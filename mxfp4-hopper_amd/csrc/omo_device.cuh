@@ -1,0 +1,116 @@
+// Device-side helpers shared by the MXFP4 kernels (gfx950 / CDNA4 only).
+//
+// Bit-level conventions used throughout:
+//   * bf16 values travel as their 16-bit patterns; two of them share a dword,
+//     element 2j in the low half, element 2j+1 in the high half.
+//   * an MXFP4 code byte holds element 2j in its low nibble and 2j+1 in its
+//     high nibble (code/kernel/per_token_quant_mxfp4.cu:256-262).
+//   * an E8M0 scale byte s stands for 2^(s-127).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace omo_hip {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// A dword of two bf16 as the vector operand of the gfx950 scaled converts.
+// The empty asm pins the value in a VGPR: without it, ROCm 7.2's compiler
+// feeds element 0 of a u32x4 to every __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16
+// that reads elements 1..3 (it emits a single dword load for all four).
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t w) {
+  asm volatile("" : "+v"(w));
+  return __builtin_bit_cast(bf16x2_t, w);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// Packed unsigned 16-bit max of both halves (v_pk_max_u16).
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  u16x2_t r = __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a), __builtin_bit_cast(u16x2_t, b));
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// DPP quad permutations: every lane reads the value of lane (quad base + sel[i]).
+// quad_perm encodings: [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E.
+__device__ __forceinline__ uint32_t dpp_quad_xor1(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t dpp_quad_xor2(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+}
+
+// Maximum over the 4 lanes of a quad (all 4 lanes must be active).
+__device__ __forceinline__ uint32_t quad_max_u32(uint32_t v) {
+  v = max(v, dpp_quad_xor1(v));
+  v = max(v, dpp_quad_xor2(v));
+  return v;
+}
+__device__ __forceinline__ float quad_fmax(float v) {
+  v = fmaxf(v, __uint_as_float(dpp_quad_xor1(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_quad_xor2(__float_as_uint(v))));
+  return v;
+}
+
+// E2M1 nibble -> bf16 bits, the reference decode
+// (code/kernel/per_token_Mxfp4ToBf16_dequant.cu:137-150): em<<6 | sign<<15,
+// +126<<7 when the exponent bits are non-zero, code 1 -> 0.5 (0x3F00).
+__device__ __forceinline__ uint32_t e2m1_to_bf16_bits(uint32_t nib) {
+  uint32_t em = nib & 7u;
+  uint32_t x = (em << 6) | ((nib & 8u) << 12);
+  x += (em & 6u) ? (126u << 7) : 0u;
+  x = (em == 1u) ? (16128u | (x & 0x8000u)) : x;
+  return x;
+}
+
+// float -> E2M1 nibble by the reference's integer round-to-nearest-even path
+// (code/kernel/per_token_quant_mxfp4.cu:103-112, 213-254). The shift in the
+// denormal adjustment reaches >= 32 for exponents <= 94; the reference runs
+// on PTX where such shifts yield 0, so the shift is clamped explicitly here
+// (v_lshrrev_b32 would otherwise use only the low 5 bits of the amount).
+__device__ __forceinline__ uint32_t e2m1_from_f32_ref(float q) {
+  const uint32_t lo = 126u;
+  uint32_t bits = __float_as_uint(q);
+  uint32_t sign = bits & 0x80000000u;
+  uint32_t e = (bits >> 23) & 0xFFu;
+  uint32_t m = bits & 0x7FFFFFu;
+  uint32_t shift = 127u - (e + 1u);
+  uint32_t dm = shift >= 32u ? 0u : ((0x400000u | (m >> 1)) >> shift);
+  m = (e < 127u) ? dm : m;
+  e = (e > lo ? e : lo) - lo;
+  uint32_t m2 = m >> 21;
+  uint32_t inc = (m2 & 1u) & (((m & 0x1FFFFFu) != 0u) | ((m2 >> 1) & 1u));
+  uint32_t r = (((e << 2) | m2) + inc) >> 1;
+  r = r > 7u ? 7u : r;
+  return ((sign >> 28) | r) & 0xFu;
+}
+
+// IEEE binary32 -> bf16 bits, round to nearest even; NaN -> 0x7FFF.
+// Stands for __floats2bfloat162_rn (per_token_Mxfp4ToBf16_dequant.cu:153).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FFFu;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Two floats in [-448, 448] (never NaN) -> two OCP E4M3 bytes, RNE, packed in
+// the low 16 bits (a in bits 0..7). v_cvt_pk_fp8_f32 on gfx950 is OCP E4M3FN
+// round-to-nearest-even; in this range it equals the __nv_fp8_e4m3(float)
+// constructor (RNE, satfinite) that the reference uses.
+__device__ __forceinline__ uint32_t fp8x2_from_f32(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
+// Exact ceil(log2(z)) for a finite normal float z > 0.
+__device__ __forceinline__ int ceil_log2_normal(float z) {
+  uint32_t b = __float_as_uint(z);
+  return (int)((b >> 23) & 0xFFu) - 127 + ((b & 0x7FFFFFu) != 0u);
+}
+
+// 2^k as a float for k in [-126, 127].
+__device__ __forceinline__ float exp2i(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
+
+}  // namespace omo_hip

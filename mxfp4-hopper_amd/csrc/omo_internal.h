@@ -1,0 +1,33 @@
+// Internal host-side launcher declarations of the MXFP4 HIP library. Each
+// launcher assumes its arguments were validated by the C-ABI layer
+// (omo_abi.hip) and only enqueues work on `stream`.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <cstring>
+
+namespace omo_hip {
+
+hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, float eps, float fp4_min,
+                                float fp4_max, hipStream_t stream);
+
+hipError_t launch_dequant_bf16(const void* q, const void* s, void* out, int64_t nbytes, hipStream_t stream);
+
+hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
+                               hipStream_t stream);
+
+hipError_t launch_mxfp4_to_fp8_col(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
+                                   float eps, hipStream_t stream);
+
+hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t N,
+                                 float eps, hipStream_t stream);
+
+hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out, float* out_s, int64_t total_rows,
+                                        int64_t N, const int32_t* lens, const int32_t* offs, const int32_t* soffs,
+                                        int64_t nsplits, int64_t max_split_len, int64_t out_capacity,
+                                        int64_t out_s_rows, float eps, hipStream_t stream);
+
+hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
+                             float eps, hipStream_t stream);
+
+}  // namespace omo_hip

@@ -1,0 +1,130 @@
+// Block-quantization helpers shared by the rowwise and dual-layout
+// BF16 -> MXFP4 kernels. The rule they implement is the reference's
+// (code/kernel/per_token_quant_mxfp4.cu:151-254); see quant.hip for the
+// derivation of the fast path.
+#pragma once
+#include <cstring>
+#include "omo_device.cuh"
+
+namespace omo_hip {
+
+// Reference scale rule from an fp32 amax (already max'ed with eps).
+// Returns the E8M0 byte; *inv receives 1/y_s.
+__device__ __forceinline__ uint32_t ref_scale(float amax, float fp4_max, float* inv) {
+  float z = fmaxf(amax / fp4_max, 1e-10f);
+  if (z == __builtin_inff()) { *inv = 0.0f; return 126u; }
+  int c = ceil_log2_normal(z);
+  if (c >= 128) { *inv = 0.0f; return 126u; }  // exp2f(128) overflows: y_s = inf
+  // 1/2^c is exact; c == 127 gives the binary32 subnormal 2^-127.
+  *inv = (c <= 126) ? exp2i(-c) : __uint_as_float(0x00400000u);
+  return (uint32_t)(c + 127) & 0xFFu;
+}
+
+// Emulation of the reference for one chunk of a quad. All four lanes of the
+// quad must call it together (DPP reduction).
+__device__ __forceinline__ void quant_chunk_ref(const u32x4& d, float eps, float fp4_min, float fp4_max,
+                                                uint32_t* codes, uint32_t* byte) {
+  const uint32_t w[4] = {d[0], d[1], d[2], d[3]};
+  float amax = eps;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    amax = fmaxf(amax, fabsf(bf16_to_f32(w[k] & 0xFFFFu)));
+    amax = fmaxf(amax, fabsf(bf16_to_f32(w[k] >> 16)));
+  }
+  amax = quad_fmax(amax);
+  float inv;
+  *byte = ref_scale(amax, fp4_max, &inv);
+  uint32_t out = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    float qx = fminf(fmaxf(bf16_to_f32(w[k] & 0xFFFFu) * inv, fp4_min), fp4_max);
+    float qy = fminf(fmaxf(bf16_to_f32(w[k] >> 16) * inv, fp4_min), fp4_max);
+    out |= (e2m1_from_f32_ref(qx) | (e2m1_from_f32_ref(qy) << 4)) << (8 * k);
+  }
+  *codes = out;
+}
+
+// Fast path for one chunk: returns the 4 code bytes; *byte gets the scale.
+// amax_bits is the quad-wide max of |x| bit patterns, < 0x7F80.
+__device__ __forceinline__ uint32_t quant_chunk_fast(const u32x4& d, uint32_t amax_bits, float eps, int c_eps,
+                                                     uint32_t* byte) {
+  float xmax = bf16_to_f32(amax_bits);
+  int c = (int)(amax_bits >> 7) - 129 + ((amax_bits & 0x7Fu) > 64u ? 1 : 0);
+  c = c < -33 ? -33 : c;
+  c = (xmax > eps) ? c : c_eps;
+  *byte = (uint32_t)(c + 127);
+  float y_s = exp2i(c);
+  uint32_t r = 0;
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[0]), y_s, 0);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[1]), y_s, 1);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[2]), y_s, 2);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[3]), y_s, 3);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t chunk_absmax_bits(const u32x4& d) {
+  uint32_t m = pk_max_u16(pk_max_u16(d[0] & 0x7FFF7FFFu, d[1] & 0x7FFF7FFFu),
+                          pk_max_u16(d[2] & 0x7FFF7FFFu, d[3] & 0x7FFF7FFFu));
+  return max(m & 0xFFFFu, m >> 16);
+}
+
+// Column variant: one lane owns a whole 32-element block given as 16 packed
+// bf16 pairs (element 2j low, 2j+1 high). Returns the 16 code bytes.
+__device__ __forceinline__ u32x4 quant_block32_fast(const uint32_t (&p)[16], uint32_t amax_bits, float eps, int c_eps,
+                                                    uint32_t* byte) {
+  float xmax = bf16_to_f32(amax_bits);
+  int c = (int)(amax_bits >> 7) - 129 + ((amax_bits & 0x7Fu) > 64u ? 1 : 0);
+  c = c < -33 ? -33 : c;
+  c = (xmax > eps) ? c : c_eps;
+  *byte = (uint32_t)(c + 127);
+  const float y_s = exp2i(c);
+  u32x4 out;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    uint32_t r = 0;
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 0]), y_s, 0);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 1]), y_s, 1);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 2]), y_s, 2);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 3]), y_s, 3);
+    out[w] = r;
+  }
+  return out;
+}
+
+__device__ __forceinline__ u32x4 quant_block32_ref(const uint32_t (&p)[16], float eps, float fp4_min, float fp4_max,
+                                                   uint32_t* byte) {
+  float amax = eps;
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    amax = fmaxf(amax, fabsf(bf16_to_f32(p[k] & 0xFFFFu)));
+    amax = fmaxf(amax, fabsf(bf16_to_f32(p[k] >> 16)));
+  }
+  float inv;
+  *byte = ref_scale(amax, fp4_max, &inv);
+  u32x4 out;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t pk = p[4 * w + k];
+      float qx = fminf(fmaxf(bf16_to_f32(pk & 0xFFFFu) * inv, fp4_min), fp4_max);
+      float qy = fminf(fmaxf(bf16_to_f32(pk >> 16) * inv, fp4_min), fp4_max);
+      o |= (e2m1_from_f32_ref(qx) | (e2m1_from_f32_ref(qy) << 4)) << (8 * k);
+    }
+    out[w] = o;
+  }
+  return out;
+}
+
+// Host-side scale exponent for amax == eps (exact
+// ceil(log2(max(fl(eps/fp4_max), 1e-10f)))).
+static inline int host_c_eps(float eps, float fp4_max) {
+  float y = eps / fp4_max;
+  float z = y > 1e-10f ? y : 1e-10f;
+  uint32_t b;
+  memcpy(&b, &z, 4);
+  return (int)((b >> 23) & 0xFFu) - 127 + ((b & 0x7FFFFFu) != 0u);
+}
+
+}  // namespace omo_hip

@@ -1,0 +1,183 @@
+// MXFP4 -> FP8 E4M3 requant, rowwise (1x128 power-of-two scales stored
+// transposed) and the transposed-output variant.
+//
+// Rowwise semantics follow omo_per_token_Mxfp4ToFp8_kernel
+// (code/kernel/per_token_Mxfp4ToFp8.cu:92-235). Per 128-element group G
+// (64 code bytes, 4 E8M0 bytes s[4G..4G+3]):
+//   g   = (uint16)(max(s) - 6)                                 :162-165
+//   y_s = fp32 with bits ((uint8)g) << 23, stored at [col*M + row] :172-180
+//   per element: bf16(code) - ((uint16)(g - s_i) << 7) (mod 2^16), as fp32,
+//   clamped by fmaxf(-448, fminf(448, .)), then E4M3 RNE.       :192-229
+// The modular subtraction is kept exactly, including its wrap for zero
+// codes (-448 when s_i <= max(s) - 7) and for max(s) < 6.
+//
+// Transposed semantics follow omo_per_token_Mxfp4ToFp8_col_kernel
+// (code/kernel/per_token_Mxfp4ToFp8_col.cu:110-301) on 128-row x 128-byte
+// tiles: per MX column c of the tile g_c = (uint8)(max(eps8, max_rows s) - 6),
+// y_s(g_c) replicated over the column's 32 outputs of scale row by (:183-212),
+// element value (bf16(code) - ((uint8)(g_c - s) << 7)) & 0x7FFF (sign
+// dropped, :244-274), clamped by fminf(fmaxf(., -448), 448), E4M3 RNE, and
+// written to [element_column * M + row] (:282-290).
+#include "omo_device.cuh"
+#include "omo_internal.h"
+
+namespace omo_hip {
+
+// ---------------------------------------------------------------- rowwise
+// Each lane converts one code dword (8 elements) into 8 FP8 bytes; 16 lanes
+// cover one group. A wave reads 256 contiguous code bytes and writes 512
+// contiguous FP8 bytes per instruction.
+template <int UNROLL>
+__global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint32_t* __restrict__ q,
+                                                           const uint32_t* __restrict__ s4,
+                                                           u32x2* __restrict__ out, float* __restrict__ out_s,
+                                                           int64_t ndw, uint32_t M, uint32_t gpr) {
+  const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
+  uint32_t c[UNROLL], sd[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const int64_t i = base + (int64_t)u * 256;
+    if (i < ndw) {
+      c[u] = __builtin_nontemporal_load(q + i);
+      sd[u] = s4[i >> 4];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const int64_t i = base + (int64_t)u * 256;
+    if (i >= ndw) continue;
+    const uint32_t s = sd[u];
+    const uint32_t smax = max(max(s & 0xFFu, (s >> 8) & 0xFFu), max((s >> 16) & 0xFFu, s >> 24));
+    const uint32_t g16 = (smax - 6u) & 0xFFFFu;
+    const uint32_t s_i = (s >> (8 * ((uint32_t)(i & 15) >> 2))) & 0xFFu;
+    const uint32_t offset = (((g16 - s_i) & 0xFFFFu) << 7) & 0xFFFFu;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t byte = (c[u] >> (8 * k)) & 0xFFu;
+      const uint32_t a0 = (e2m1_to_bf16_bits(byte & 0xFu) - offset) & 0xFFFFu;
+      const uint32_t a1 = (e2m1_to_bf16_bits(byte >> 4) - offset) & 0xFFFFu;
+      const float f0 = fmaxf(-448.0f, fminf(448.0f, bf16_to_f32(a0)));
+      const float f1 = fmaxf(-448.0f, fminf(448.0f, bf16_to_f32(a1)));
+      const uint32_t pr = fp8x2_from_f32(f0, f1);
+      if (k < 2) lo |= pr << (16 * k); else hi |= pr << (16 * (k - 2));
+    }
+    u32x2 o;
+    o[0] = lo;
+    o[1] = hi;
+    __builtin_nontemporal_store(o, out + i);
+    if ((i & 15) == 0) {
+      const uint32_t G = (uint32_t)(i >> 4);
+      const uint32_t row = G / gpr, col = G - row * gpr;
+      out_s[(int64_t)col * M + row] = __uint_as_float((g16 & 0xFFu) << 23);
+    }
+  }
+}
+
+hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
+                               hipStream_t stream) {
+  const int64_t ndw = M * Kb / 4;
+  if (ndw == 0) return hipSuccess;
+  constexpr int U = 4;
+  const int64_t blocks = (ndw + 256 * U - 1) / (256 * U);
+  hipLaunchKernelGGL((mxfp4_to_fp8_kernel<U>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const uint32_t*>(q), static_cast<const uint32_t*>(s), static_cast<u32x2*>(out),
+                     out_s, ndw, (uint32_t)M, (uint32_t)(Kb / 64));
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------ transposed
+// One 256-thread block per 128-row x 128-byte tile. The code tile and its
+// 128x8 scale bytes are staged in LDS; each thread then produces one output
+// row segment (one element column of the tile, 128 contiguous FP8 bytes =
+// a full 128 B line).
+constexpr int kColTile = 128;
+constexpr int kColPitch = kColTile + 4;
+
+__global__ __launch_bounds__(256) void mxfp4_to_fp8_col_kernel(const uint8_t* __restrict__ q,
+                                                               const uint8_t* __restrict__ s,
+                                                               uint8_t* __restrict__ out, float* __restrict__ out_s,
+                                                               int64_t M, int64_t Kb, uint32_t eps8) {
+  __shared__ uint8_t tile[kColTile * kColPitch];
+  __shared__ uint8_t stile[kColTile][8];
+  __shared__ uint32_t gpart[4][8];
+  __shared__ uint32_t gcol[8];
+  const int t = threadIdx.x;
+  const int64_t bx = blockIdx.x, by = blockIdx.y;
+  const int64_t row0 = by * kColTile;
+  const int64_t sstride = Kb / 16;
+  // codes: 128 rows x 128 B = 1024 chunks of 16 B
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int cidx = t + 256 * k;
+    const int r = cidx >> 3, c16 = cidx & 7;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(q + (row0 + r) * Kb + bx * kColTile + c16 * 16);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(tile + r * kColPitch + c16 * 16);
+    dst[0] = v[0];
+    dst[1] = v[1];
+    dst[2] = v[2];
+    dst[3] = v[3];
+  }
+  if (t < kColTile) {
+    const u32x2 sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * sstride + bx * 8);
+    *reinterpret_cast<u32x2*>(&stile[t][0]) = sv;
+  }
+  __syncthreads();
+  // per MX column: max over 128 rows (seeded with (uint8)eps)
+  {
+    const int c = t & 7, rq = t >> 3;  // rows 4rq..4rq+3
+    uint32_t m = eps8;
+#pragma unroll
+    for (int j = 0; j < 4; j++) m = max(m, (uint32_t)stile[rq * 4 + j][c]);
+    m = max(m, (uint32_t)__shfl_xor((int)m, 8));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 16));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 32));
+    if ((t & 63) < 8) gpart[t >> 6][c] = m;
+  }
+  __syncthreads();
+  if (t < 8) {
+    const uint32_t m = max(max(gpart[0][t], gpart[1][t]), max(gpart[2][t], gpart[3][t]));
+    gcol[t] = (m - 6u) & 0xFFu;
+  }
+  __syncthreads();
+  // scale row by: 256 floats, entry j holds column j/32
+  out_s[by * (Kb * 2) + bx * 256 + t] = __uint_as_float(gcol[t >> 5] << 23);
+  // outputs: thread t -> element column e = t of the tile (byte t/2, nibble t&1)
+  const int b = t >> 1, h = t & 1, cblk = b >> 4;
+  const uint32_t g = gcol[cblk];
+  uint8_t* orow = out + (bx * 256 + t) * M + row0;
+#pragma unroll
+  for (int m16 = 0; m16 < kColTile; m16 += 16) {
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int r = m16 + j;
+      const uint32_t val = tile[r * kColPitch + b];
+      const uint32_t nib = h ? (val >> 4) : (val & 0xFu);
+      const uint32_t adj = (g - (uint32_t)stile[r][cblk]) & 0xFFu;
+      const uint32_t a = ((e2m1_to_bf16_bits(nib) - (adj << 7)) & 0xFFFFu) & 0x7FFFu;
+      const float f = fminf(fmaxf(bf16_to_f32(a), -448.0f), 448.0f);
+      const uint32_t byte = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f, f, 0, false) & 0xFFu;
+      w[j >> 2] |= byte << (8 * (j & 3));
+    }
+    u32x4 o;
+    o[0] = w[0];
+    o[1] = w[1];
+    o[2] = w[2];
+    o[3] = w[3];
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(orow + m16));
+  }
+}
+
+hipError_t launch_mxfp4_to_fp8_col(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
+                                   float eps, hipStream_t stream) {
+  if (M == 0 || Kb == 0) return hipSuccess;
+  uint32_t eps8 = 0;
+  if (eps > 0.0f) eps8 = eps >= 255.0f ? 255u : (uint32_t)eps;  // (uint8_t)eps, truncating
+  dim3 grid((unsigned)(Kb / kColTile), (unsigned)(M / kColTile));
+  hipLaunchKernelGGL(mxfp4_to_fp8_col_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
+                     static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, M, Kb, eps8);
+  return hipGetLastError();
+}
+
+}  // namespace omo_hip

@@ -1,0 +1,259 @@
+"""``omo``: drop-in for the reference's pybind module of the same name.
+
+The reference binds seven functions (code/kernel/ops.cu:27-41) plus imports an
+eighth from its Python API (code/kernel/api/mxfp4_dequant.py:1). This module
+exposes the same names, keyword names and argument order. Each function
+runs the reference host checks (``CHECK_INPUT`` = on the GPU and contiguous,
+``CHECK_EQ`` on sizes; failures raise ``RuntimeError``), then calls the
+gfx950 HIP library through its C ABI (include/omo_mxfp4.h) on the current
+HIP stream of the input's device. Outputs are preallocated by the caller and
+written in place; nothing is returned, as in the reference.
+
+Deliberate differences from the reference host code, each where the
+reference would launch a kernel on memory it does not own or silently do
+nothing:
+  * wrong tensor dtypes raise ``RuntimeError`` (the reference's dispatch
+    macro skips the launch);
+  * ``scale_ue8m0=True`` and column-major scale tensors raise
+    ``NotImplementedError`` (the reference routes them to a kernel launched
+    with a thread count it does not support, per_token_quant_mxfp4.cu:287,418);
+  * undersized outputs, shapes the reference kernels cannot index (see the
+    C ABI), and NaN / non-finite constants raise ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._abi import check as _check
+from ._abi import lib as _lib
+
+__all__ = [
+    "omo_per_token_group_quant_fp4",
+    "omo_per_token_Mxfp4ToBf16_dequant",
+    "omo_per_token_Mxfp4ToBf16ToFp8",
+    "omo_per_token_group_quant_fp4_fused_ToFp8",
+    "omo_per_token_Mxfp4RowToBf16ToFp8Col",
+    "omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit",
+    "omo_per_token_Mxfp4ToFp8_col",
+    "omo_per_token_Mxfp4ToFp8",
+    "omo_quant_mxfp4_dual",
+]
+
+_FP8 = torch.float8_e4m3fn
+
+
+def _check_input(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _check_eq(a, b, what: str) -> None:
+    if a != b:
+        raise RuntimeError(f"Expected {what} ({a} vs. {b})")
+
+
+def _check_dtype(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must have dtype {dtype}, got {t.dtype}")
+
+
+def _same_device(ref: torch.Tensor, *others) -> None:
+    for o in others:
+        if o.device != ref.device:
+            raise RuntimeError(f"all tensors must be on {ref.device}, got {o.device}")
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+class _on_device:
+    """Make ``t``'s device current for the launch (the library launches on
+    the current HIP device) and yield its current stream handle."""
+
+    def __init__(self, t: torch.Tensor):
+        self.dev = t.device
+
+    def __enter__(self):
+        self.prev = torch.cuda.current_device()
+        if self.dev.index is not None and self.dev.index != self.prev:
+            torch.cuda.set_device(self.dev)
+        return torch.cuda.current_stream(self.dev).cuda_stream
+
+    def __exit__(self, *exc):
+        if torch.cuda.current_device() != self.prev:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def omo_per_token_group_quant_fp4(input, output_q, output_s, group_size, eps, fp4_min, fp4_max, scale_ue8m0):
+    """BF16 -> MXFP4 quantize, 1x32 blocks over the flat tensor.
+    Reference: omo::omo_per_token_group_quant_fp4, code/kernel/per_token_quant_mxfp4.cu:387-487."""
+    _check_input(input, "input")
+    _check_input(output_q, "output_q")
+    _check_eq(input.numel() % group_size, 0, "input.numel() % group_size == 0")
+    _check_eq(output_s.dim(), 2, "output_s.dim() == 2")
+    _same_device(input, output_q, output_s)
+    if output_s.stride(0) < output_s.stride(1):
+        raise NotImplementedError("column-major scale tensors are not supported")
+    if not output_s.is_contiguous():
+        raise RuntimeError("output_s must be contiguous")
+    _check_dtype(input, torch.bfloat16, "input")
+    _check_dtype(output_q, torch.uint8, "output_q")
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_per_token_group_quant_fp4(
+            input.data_ptr(), input.numel(), output_q.data_ptr(), _nbytes(output_q), output_s.data_ptr(),
+            _nbytes(output_s), int(group_size), float(eps), float(fp4_min), float(fp4_max), int(bool(scale_ue8m0)),
+            stream))
+
+
+def omo_per_token_Mxfp4ToBf16_dequant(input, input_s, output_q, output_s, group_size, eps, fp4_min, fp4_max,
+                                      scale_ue8m0):
+    """MXFP4 -> BF16 dequant over the flat code tensor.
+    Reference: omo::omo_per_token_Mxfp4ToBf16_dequant, code/kernel/per_token_Mxfp4ToBf16_dequant.cu:164-238."""
+    _check_input(input, "input")
+    _check_input(output_q, "output_q")
+    _check_eq(input.numel() % 128, 0, "input.numel() % group_size == 0")
+    _check_eq(output_s.dim(), 2, "output_s.dim() == 2")
+    _same_device(input, input_s, output_q)
+    _check_input(input_s, "input_s")
+    _check_dtype(input, torch.uint8, "input")
+    _check_dtype(input_s, torch.uint8, "input_s")
+    _check_dtype(output_q, torch.bfloat16, "output_q")
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_per_token_Mxfp4ToBf16_dequant(
+            input.data_ptr(), input.numel(), input_s.data_ptr(), input_s.numel(), output_q.data_ptr(),
+            output_q.numel(), output_s.data_ptr(), _nbytes(output_s), int(group_size), float(eps), float(fp4_min),
+            float(fp4_max), int(bool(scale_ue8m0)), stream))
+
+
+def _requant_args(name, input, input_s, output_q, output_s):
+    _check_input(input, "input")
+    _check_input(output_q, "output_q")
+    _check_eq(input.numel() % 128, 0, "input.numel() % group_size == 0")
+    _check_eq(output_s.dim(), 2, "output_s.dim() == 2")
+    if input.dim() != 2:
+        raise RuntimeError(f"{name}: input must be 2-D [M, K/2]")
+    _same_device(input, input_s, output_q, output_s)
+    _check_input(input_s, "input_s")
+    _check_input(output_s, "output_s")
+    _check_dtype(input, torch.uint8, "input")
+    _check_dtype(input_s, torch.uint8, "input_s")
+    _check_dtype(output_q, _FP8, "output_q")
+    _check_dtype(output_s, torch.float32, "output_s")
+
+
+def _requant_rowwise(fn, name, input, input_s, output_q, output_s, group_size, eps, fp4_min, fp4_max, scale_ue8m0):
+    _requant_args(name, input, input_s, output_q, output_s)
+    with _on_device(input) as stream:
+        _check(fn(input.data_ptr(), input.size(0), input.size(1), input_s.data_ptr(), input_s.numel(),
+                  output_q.data_ptr(), output_q.numel(), output_s.data_ptr(), output_s.numel(), int(group_size),
+                  float(eps), float(fp4_min), float(fp4_max), int(bool(scale_ue8m0)), stream))
+
+
+def omo_per_token_Mxfp4ToFp8(input, input_s, output_q, output_s, group_size, eps, fp4_min, fp4_max, scale_ue8m0):
+    """MXFP4 -> FP8 E4M3 rowwise with 1x128 power-of-two scales, stored [K/64, M].
+    Reference: omo::omo_per_token_Mxfp4ToFp8, code/kernel/per_token_Mxfp4ToFp8.cu:238-309."""
+    _requant_rowwise(_lib.omo_hip_per_token_Mxfp4ToFp8, "omo_per_token_Mxfp4ToFp8", input, input_s, output_q,
+                     output_s, group_size, eps, fp4_min, fp4_max, scale_ue8m0)
+
+
+def omo_per_token_Mxfp4ToBf16ToFp8(input, input_s, output_q, output_s, group_size, eps, fp4_min, fp4_max,
+                                   scale_ue8m0):
+    """Bound by the reference (code/kernel/ops.cu:32-33) without a shipped source;
+    same signature and call site shape as omo_per_token_Mxfp4ToFp8, computed by it."""
+    _requant_rowwise(_lib.omo_hip_per_token_Mxfp4ToBf16ToFp8, "omo_per_token_Mxfp4ToBf16ToFp8", input, input_s,
+                     output_q, output_s, group_size, eps, fp4_min, fp4_max, scale_ue8m0)
+
+
+def omo_per_token_Mxfp4ToFp8_col(input, input_s, output_q, output_s, group_size, eps, fp4_min, fp4_max, scale_ue8m0):
+    """MXFP4 rowwise -> FP8 transposed [K, M] with 128-row power-of-two scales (sign dropped).
+    Reference: omo::omo_per_token_Mxfp4ToFp8_col, code/kernel/per_token_Mxfp4ToFp8_col.cu:305-384."""
+    _requant_args("omo_per_token_Mxfp4ToFp8_col", input, input_s, output_q, output_s)
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_per_token_Mxfp4ToFp8_col(
+            input.data_ptr(), input.size(0), input.size(1), input_s.data_ptr(), input_s.numel(), output_q.data_ptr(),
+            output_q.numel(), output_s.data_ptr(), output_s.numel(), int(group_size), float(eps), float(fp4_min),
+            float(fp4_max), int(bool(scale_ue8m0)), stream))
+
+
+def omo_per_token_Mxfp4RowToBf16ToFp8Col(input, input_s, output_q, output_s, eps):
+    """MXFP4 rowwise -> FP8 columnwise [N, M] + scale_inv [ceil(M/128), N] (amax/448).
+    Reference: omo::omo_per_token_Mxfp4RowToBf16ToFp8Col, code/kernel/per_token_Mxfp4RowToBf16ToFp8Col.cu:204-246."""
+    _check_input(input, "input")
+    _check_input(output_q, "output_q")
+    _check_eq(input.dim(), 2, "input.dim() == 2")
+    _check_eq(output_q.dim(), 2, "output_q.dim() == 2")
+    _same_device(input, input_s, output_q, output_s)
+    _check_input(input_s, "input_s")
+    _check_input(output_s, "output_s")
+    _check_dtype(input, torch.uint8, "input")
+    _check_dtype(input_s, torch.uint8, "input_s")
+    _check_dtype(output_q, _FP8, "output_q")
+    _check_dtype(output_s, torch.float32, "output_s")
+    if input_s.dim() != 2 or output_s.dim() != 2:
+        raise RuntimeError("input_s and output_s must be 2-D")
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(
+            input.data_ptr(), input.size(0), input.size(1), input_s.data_ptr(), input_s.size(0), input_s.size(1),
+            output_q.data_ptr(), output_q.size(0), output_q.size(1), output_s.data_ptr(), output_s.size(0),
+            output_s.size(1), float(eps), stream))
+
+
+def omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(input, input_s, output_q, output_s, m_splits, split_offsets,
+                                                scale_offsets, max_split_len, eps):
+    """Per-split (MoE expert) MXFP4 rowwise -> FP8 columnwise with power-of-two scales.
+    ``m_splits``, ``split_offsets``, ``scale_offsets`` are int32 device tensors.
+    Reference: omo::omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit,
+    code/kernel/per_token_Mxfp4RowToBf16ToFp8Col_msplit.cu:232-283."""
+    for t, n in ((input, "input"), (output_q, "output_q"), (m_splits, "m_splits"), (split_offsets, "split_offsets"),
+                 (scale_offsets, "scale_offsets")):
+        _check_input(t, n)
+    _same_device(input, input_s, output_q, output_s, m_splits, split_offsets, scale_offsets)
+    _check_input(input_s, "input_s")
+    _check_input(output_s, "output_s")
+    if input.dim() != 2:
+        raise RuntimeError("input must be 2-D [total_M, N/2]")
+    _check_dtype(input, torch.uint8, "input")
+    _check_dtype(input_s, torch.uint8, "input_s")
+    _check_dtype(output_q, _FP8, "output_q")
+    _check_dtype(output_s, torch.float32, "output_s")
+    for t, n in ((m_splits, "m_splits"), (split_offsets, "split_offsets"), (scale_offsets, "scale_offsets")):
+        _check_dtype(t, torch.int32, n)
+        if t.numel() != m_splits.numel():
+            raise RuntimeError(f"{n} must have one entry per split")
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(
+            input.data_ptr(), input.size(0), input.size(1), input_s.data_ptr(), input_s.numel(), output_q.data_ptr(),
+            output_q.numel(), output_s.data_ptr(), output_s.numel(), m_splits.data_ptr(), split_offsets.data_ptr(),
+            scale_offsets.data_ptr(), m_splits.numel(), int(max_split_len), float(eps), stream))
+
+
+def omo_per_token_group_quant_fp4_fused_ToFp8(input, output_q, output_s, output_bf16_q, output_bf16_s, group_size,
+                                              eps, fp4_min, fp4_max, scale_ue8m0):
+    """Bound by the reference (code/kernel/ops.cu:34-35) but shipped without a
+    source or any caller, so its semantics are unknown; it is not implemented."""
+    raise NotImplementedError(
+        "omo_per_token_group_quant_fp4_fused_ToFp8: the reference ships no implementation of this binding")
+
+
+def omo_quant_mxfp4_dual(input, row_q, row_s, col_q, col_s, eps=1e-10):
+    """Fused rowwise + columnwise BF16 -> MXFP4 quantize of a 2-D [M, K] tensor.
+    col_q/col_s equal omo_per_token_group_quant_fp4 applied to input.T.contiguous(),
+    the columnwise path of TE's _QuantizeFunc (code/transformer_engine-2.8.diff:1463-1466)."""
+    for t, n in ((input, "input"), (row_q, "row_q"), (row_s, "row_s"), (col_q, "col_q"), (col_s, "col_s")):
+        _check_input(t, n)
+    _same_device(input, row_q, row_s, col_q, col_s)
+    if input.dim() != 2:
+        raise RuntimeError("input must be 2-D")
+    _check_dtype(input, torch.bfloat16, "input")
+    for t, n in ((row_q, "row_q"), (row_s, "row_s"), (col_q, "col_q"), (col_s, "col_s")):
+        _check_dtype(t, torch.uint8, n)
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_quant_mxfp4_dual(
+            input.data_ptr(), input.size(0), input.size(1), row_q.data_ptr(), row_q.numel(), row_s.data_ptr(),
+            row_s.numel(), col_q.data_ptr(), col_q.numel(), col_s.data_ptr(), col_s.numel(), float(eps), stream))

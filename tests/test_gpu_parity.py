@@ -1,0 +1,374 @@
+"""GPU parity: every HIP entry point against the CPU oracle, bit for bit.
+
+Inputs are generated on the host (seeded), copied to the device, run through
+the `omo` binding (the C ABI of libomo_mxfp4.so) and compared byte for byte
+with oracle/mxfp4_oracle.c on the same bytes.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits_u16, bits_u8, from_u16
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _omo():
+    import omo
+    return omo
+
+
+# ----------------------------------------------------------------- inputs
+def domain_blocks():
+    """Every finite bf16 value v with |v| <= 6*2^c, for every reachable scale
+    exponent c in [-33, 126], placed after an anchor element that fixes the
+    block's scale to c. Returns (bf16 bits, expected scale bytes)."""
+    vals, scales = [], []
+    for c in range(-33, 127):
+        anchor = 0x7F7F if c == 126 else 0x40C0 + (c << 7)
+        mags = np.arange(anchor + 1, dtype=np.uint32)
+        v = np.concatenate([mags, mags | 0x8000]).astype(np.uint16)
+        nblk = -(-v.size // 31)
+        pad = np.zeros(nblk * 31, np.uint16)
+        pad[: v.size] = v
+        blk = np.empty((nblk, 32), np.uint16)
+        blk[:, 0] = anchor
+        blk[:, 1:] = pad.reshape(nblk, 31)
+        vals.append(blk.reshape(-1))
+        scales.append(np.full(nblk, c + 127, np.uint8))
+    return np.concatenate(vals), np.concatenate(scales)
+
+
+def special_blocks():
+    """Blocks exercising the reference's special cases."""
+    inf, ninf, qnan, snan, nqnan = 0x7F80, 0xFF80, 0x7FC0, 0x7F81, 0xFFC0
+    one, six, half = 0x3F80, 0x40C0, 0x3F00
+    rows = [
+        [0] * 32,                                    # all zero -> scale 94
+        [0x8000] * 32,                               # all -0
+        [1, 0x8001, 0x007F, 0x807F] + [0] * 28,      # denormals only
+        [qnan] + [one] * 31,                         # NaN ignored by amax, NaN -> 0xF
+        [snan, nqnan] + [six] * 30,                  # signalling / negative NaN
+        [qnan] * 32,                                 # NaN only: amax = eps
+        [inf] + [one, 0x8000 | one, 0, 0x8000] * 7 + [one, one, ninf],  # inf: scale 126
+        [ninf] * 32,
+        [inf, qnan] + [half] * 30,                   # inf and NaN together
+        [0x7F7F] + [0x0001] * 31,                    # max finite with denormals
+        [0x7F40] + [one] * 31,                       # 1.5*2^127: exact power-of-two quotient
+        [0x40C1] + [0x3E80, 0x3F40, 0x3FA0, 0x3FE0, 0x4020, 0x4060, 0x40A0, 0x40B0] * 3 + [0] * 7,
+        [0x40C0] + [0x3E80, 0x3F40, 0x3FA0, 0x3FE0, 0x4020, 0x4060, 0x40A0, 0x40B0] * 3 + [0] * 7,
+        [0x2F00] * 32,                               # below eps*6: eps dominates
+        [0x3040] + [0x2FFF] * 31,                    # 6*2^-33 anchor
+    ]
+    return np.array(rows, dtype=np.uint16).reshape(-1)
+
+
+def run_quant(x_bits, dev, eps=1e-10, fmin=-6.0, fmax=6.0, shape=None):
+    omo = _omo()
+    x = from_u16(x_bits, dev)
+    if shape is not None:
+        x = x.view(shape)
+    M = x.shape[0] if x.dim() > 1 else 1
+    q = torch.empty(x.numel() // 2, dtype=torch.uint8, device=dev)
+    s = torch.empty((M, x.numel() // 32 // M), dtype=torch.uint8, device=dev)
+    omo.omo_per_token_group_quant_fp4(x, q, s, 32, eps, fmin, fmax, False)
+    torch.cuda.synchronize()
+    return bits_u8(q), bits_u8(s).reshape(-1)
+
+
+# ----------------------------------------------------------------- quantize
+@pytest.mark.parametrize("shape,std,seed", [
+    ((1, 32), 1.0, 1), ((3, 64), 1.0, 2), ((128, 256), 3.0, 3), ((257, 7168), 1.0, 4),
+    ((64, 1056), 1e-3, 5), ((2, 8192 * 4 + 96), 1e4, 6), ((1000, 96), 1e-30, 7),
+])
+def test_quant_seeded(oracle, dev, shape, std, seed):
+    _say("quant seeded", shape, std, seed)
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(shape, generator=g) * std).to(torch.bfloat16)
+    xb = bits_u16(x).reshape(-1)
+    q, s = run_quant(xb, dev, shape=shape)
+    eq, es = oracle.quant_mxfp4(xb)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(q, eq)
+
+
+def test_quant_special_values(oracle, dev):
+    _say("quant specials")
+    xb = special_blocks()
+    q, s = run_quant(xb, dev)
+    eq, es = oracle.quant_mxfp4(xb)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(q, eq)
+    assert s[0] == 94 and s[6] == 126
+
+
+def test_quant_full_domain(oracle, dev):
+    """All bf16 values under every reachable scale exponent, through the
+    production kernel (fast path for every block)."""
+    _say("quant full domain")
+    xb, exp_s = domain_blocks()
+    q, s = run_quant(xb, dev)
+    eq, es = oracle.quant_mxfp4(xb)
+    np.testing.assert_array_equal(es, exp_s)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(q, eq)
+
+
+@pytest.mark.parametrize("eps,fmin,fmax", [
+    (1e-10, -4.0, 4.0), (1e-10, -6.5, 6.5), (0.0, -6.0, 6.0), (1e-3, -6.0, 6.0), (1.0, -6.0, 6.0),
+    (-1.0, -6.0, 6.0), (3e-38, -6.0, 6.0), (1e-10, -1.0, 6.0), (1e-10, -6.0, 0.7),
+])
+def test_quant_parameters(oracle, dev, eps, fmin, fmax):
+    _say("quant params", eps, fmin, fmax)
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn((64, 512), generator=g) * torch.logspace(-3, 3, 512)).to(torch.bfloat16)
+    xb = np.concatenate([bits_u16(x).reshape(-1), special_blocks()])
+    q, s = run_quant(xb, dev, eps=eps, fmin=fmin, fmax=fmax)
+    eq, es = oracle.quant_mxfp4(xb, eps=eps, fp4_min=fmin, fp4_max=fmax)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(q, eq)
+
+
+def test_quant_cfg2_north_star(oracle, dev):
+    """8192 x 7168 activations with outlier channels (the benchmark input)."""
+    import omo_workloads as wl
+    _say("quant cfg2 8192x7168")
+    x = wl.activations_with_outliers(8192, 7168, seed=2026, device="cpu")
+    xb = bits_u16(x).reshape(-1)
+    q, s = run_quant(xb, dev, shape=(8192, 7168))
+    eq, es = oracle.quant_mxfp4(xb)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(q, eq)
+
+
+def test_quant_wrapper_and_determinism(oracle, dev):
+    from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
+    _say("quant wrapper")
+    x = torch.randn((96, 7168), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
+    q1, s1 = omo_per_token_group_quant_mxfp4(x)
+    q2, s2 = omo_per_token_group_quant_mxfp4(x)
+    assert q1.shape == (96, 3584) and s1.shape == (96, 224)
+    assert q1.dtype == torch.uint8 and s1.dtype == torch.uint8
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+    eq, es = oracle.quant_mxfp4(bits_u16(x).reshape(-1))
+    np.testing.assert_array_equal(bits_u8(q1).reshape(-1), eq)
+    np.testing.assert_array_equal(bits_u8(s1).reshape(-1), es)
+    q0, s0 = omo_per_token_group_quant_mxfp4(x[:0])
+    assert q0.shape == (0, 3584) and s0.shape == (0, 224)
+
+
+# ------------------------------------------------------------------ dequant
+def run_dequant(q, s, dev):
+    omo = _omo()
+    qt = torch.from_numpy(q).to(dev)
+    st = torch.from_numpy(s).to(dev)
+    out = torch.empty(q.size * 2, dtype=torch.bfloat16, device=dev)
+    unused = torch.empty((1, 1), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4ToBf16_dequant(qt, st, out, unused, 32, 1e-10, -6.0, 6.0, False)
+    torch.cuda.synchronize()
+    return bits_u16(out).reshape(-1)
+
+
+def test_dequant_all_bytes_all_scales(oracle, dev):
+    _say("dequant 256 bytes x 256 scales")
+    q = np.tile(np.arange(256, dtype=np.uint8), 256 * 16)  # each scale covers 16 bytes
+    s = np.repeat(np.arange(256, dtype=np.uint8), 256)
+    got = run_dequant(q, s, dev)
+    np.testing.assert_array_equal(got, oracle.dequant_bf16(q, s))
+
+
+@pytest.mark.parametrize("M,K,seed", [(4, 128, 1), (4096, 4096, 2), (4096, 7168, 3), (33, 1024, 4)])
+def test_dequant_roundtrip_seeded(oracle, dev, M, K, seed):
+    _say("dequant seeded", M, K)
+    x = torch.randn((M, K), generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16)
+    q, s = oracle.quant_mxfp4(bits_u16(x).reshape(-1))
+    got = run_dequant(q, s, dev)
+    np.testing.assert_array_equal(got, oracle.dequant_bf16(q, s))
+
+
+def test_dequant_wrapper_dtypes(oracle, dev):
+    from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToBf16_dequant_wrapper
+    _say("dequant wrapper")
+    x = torch.randn((64, 512), generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    q, s = oracle.quant_mxfp4(bits_u16(x).reshape(-1))
+    qt = torch.from_numpy(q).view(64, 256).to(dev)
+    st = torch.from_numpy(s).view(64, 16).to(dev)
+    ref = oracle.dequant_bf16(q, s)
+    y = omo_per_token_mxfp4ToBf16_dequant_wrapper(qt, st, torch.bfloat16)
+    assert y.shape == (64, 512) and y.dtype == torch.bfloat16
+    np.testing.assert_array_equal(bits_u16(y).reshape(-1), ref)
+    y32 = omo_per_token_mxfp4ToBf16_dequant_wrapper(qt, st, torch.float32)
+    assert y32.dtype == torch.float32
+    assert torch.equal(y32.cpu(), from_u16(ref).view(64, 512).float())
+
+
+# ---------------------------------------------------------- FP8 requant rows
+def scale_spread_payload(M, Kb, seed, spread=16):
+    """Random codes with block scales spread wide within each 128-group, so
+    the wrap cases (zero code with s <= max-7, max < 6) occur."""
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 256, size=(M, Kb), dtype=np.uint8)
+    q[rng.random((M, Kb)) < 0.2] = 0
+    base = rng.integers(0, 256, size=(M, Kb // 64, 1))
+    s = np.clip(base + rng.integers(-spread, 1, size=(M, Kb // 64, 4)), 0, 255).astype(np.uint8)
+    return q, s.reshape(M, Kb // 16)
+
+
+def run_to_fp8(q, s, dev, fn="omo_per_token_Mxfp4ToFp8"):
+    omo = _omo()
+    M, Kb = q.shape
+    qt = torch.from_numpy(q).to(dev)
+    st = torch.from_numpy(np.ascontiguousarray(s)).to(dev)
+    out = torch.empty((M, 2 * Kb), dtype=FP8, device=dev)
+    outs = torch.empty((Kb // 64, M), dtype=torch.float32, device=dev)
+    getattr(omo, fn)(qt, st, out, outs, 128, 1e-10, -6.0, 6.0, False)
+    torch.cuda.synchronize()
+    return bits_u8(out), outs.cpu().numpy()
+
+
+@pytest.mark.parametrize("fn", ["omo_per_token_Mxfp4ToFp8", "omo_per_token_Mxfp4ToBf16ToFp8"])
+@pytest.mark.parametrize("M,Kb,seed,spread", [(2, 64, 1, 16), (130, 3584, 2, 16), (64, 640, 3, 255), (8, 192, 4, 3)])
+def test_to_fp8_rowwise(oracle, dev, fn, M, Kb, seed, spread):
+    _say(fn, M, Kb, spread)
+    q, s = scale_spread_payload(M, Kb, seed, spread)
+    out, outs = run_to_fp8(q, s, dev, fn)
+    eo, es = oracle.mxfp4_to_fp8(q, s)
+    np.testing.assert_array_equal(out, eo)
+    np.testing.assert_array_equal(outs.view(np.uint32), es.view(np.uint32))
+
+
+def test_to_fp8_rowwise_rejects_reference_invalid_shapes(dev):
+    """The reference host checks input.numel() % 128 == 0
+    (code/kernel/per_token_Mxfp4ToFp8.cu:259); the binding raises RuntimeError."""
+    _say("to_fp8 invalid shapes")
+    q, s = scale_spread_payload(7, 192, 1)
+    with pytest.raises(RuntimeError):
+        run_to_fp8(q, s, dev)
+
+
+def test_to_fp8_rowwise_cfg4(oracle, dev):
+    _say("to_fp8 cfg4 4096x7168")
+    x = torch.randn((4096, 7168), generator=torch.Generator().manual_seed(44)).to(torch.bfloat16)
+    q, s = oracle.quant_mxfp4(bits_u16(x).reshape(-1))
+    q = q.reshape(4096, 3584)
+    out, outs = run_to_fp8(q, s, dev)
+    eo, es = oracle.mxfp4_to_fp8(q, s)
+    np.testing.assert_array_equal(out, eo)
+    np.testing.assert_array_equal(outs.view(np.uint32), es.view(np.uint32))
+
+
+def test_to_fp8_wrapper_split(oracle, dev):
+    from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToFp8_wrapper
+    _say("to_fp8 wrapper with m_splits")
+    q, s = scale_spread_payload(300, 3584, 7)
+    qt, st = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
+    xs, ss = omo_per_token_mxfp4ToFp8_wrapper(qt, st, [100, 0, 200])
+    eo, es = oracle.mxfp4_to_fp8(q, s)
+    assert [t.shape for t in xs] == [(100, 7168), (0, 7168), (200, 7168)]
+    assert [t.shape for t in ss] == [(56, 100), (56, 0), (56, 200)]
+    np.testing.assert_array_equal(bits_u8(torch.cat(xs)), eo)
+    np.testing.assert_array_equal(torch.cat(ss, 1).cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+# ------------------------------------------------------- FP8 requant columns
+@pytest.mark.parametrize("M,Kb,seed,spread,eps", [(128, 128, 1, 16, 1e-10), (256, 3584, 2, 255, 1e-10),
+                                                  (384, 256, 3, 8, 200.0)])
+def test_to_fp8_col(oracle, dev, M, Kb, seed, spread, eps):
+    _say("to_fp8_col", M, Kb, spread, eps)
+    omo = _omo()
+    q, s = scale_spread_payload(M, Kb, seed, spread)
+    qt, st = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
+    out = torch.empty((2 * Kb, M), dtype=FP8, device=dev)
+    outs = torch.empty((M // 128, 2 * Kb), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4ToFp8_col(qt, st, out, outs, 128, eps, -6.0, 6.0, False)
+    torch.cuda.synchronize()
+    eo, es = oracle.mxfp4_to_fp8_col(q, s, eps=eps)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+# ------------------------------------------------------- row -> col (dense)
+def payload_from_normal(M, K, seed, std=1.0):
+    import oracle as o
+    x = (torch.randn((M, K), generator=torch.Generator().manual_seed(seed)) * std).to(torch.bfloat16)
+    q, s = o.quant_mxfp4(bits_u16(x).reshape(-1))
+    return q.reshape(M, K // 2), s.reshape(M, K // 32)
+
+
+@pytest.mark.parametrize("M,N,seed", [(128, 128, 1), (300, 7168, 2), (1, 64, 3), (129, 4096, 4), (1000, 2048, 5)])
+def test_row_to_fp8_col_dense(oracle, dev, M, N, seed):
+    _say("row_to_fp8_col", M, N)
+    from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4RowToBf16ToFp8Col_wrapper
+    q, s = payload_from_normal(M, N, seed)
+    out, outs = omo_per_token_mxfp4RowToBf16ToFp8Col_wrapper(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev))
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s)
+    assert out.shape == (N, M) and outs.shape == ((M + 127) // 128, N)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+def test_row_to_fp8_col_wide_scales(oracle, dev):
+    """Random codes and scale bytes over the full 0..255 range (inf / NaN /
+    subnormal dequantized values)."""
+    _say("row_to_fp8_col wide scales")
+    omo = _omo()
+    rng = np.random.default_rng(3)
+    M, N = 256, 512
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(0, 256, size=(M, N // 32), dtype=np.uint8)
+    out = torch.empty((N, M), dtype=FP8, device=dev)
+    outs = torch.empty((2, N), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+# ------------------------------------------------------- row -> col (msplit)
+@pytest.mark.parametrize("splits,N", [([1, 127, 128, 300], 256), ([0, 5, 0, 2048, 129], 7168), ([128], 128),
+                                      ([2000, 1800, 2300, 2100], 2048)])
+def test_row_to_fp8_col_msplit(oracle, dev, splits, N):
+    _say("msplit", splits, N)
+    from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper
+    M = sum(splits)
+    q, s = payload_from_normal(M, N, sum(splits) % 97)
+    ys, ss = omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper(torch.from_numpy(q).to(dev),
+                                                                 torch.from_numpy(s).to(dev), splits)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    off, soff = 0, 0
+    for i, m in enumerate(splits):
+        assert ys[i].shape == (N, m)
+        assert ss[i].shape == ((m + 127) // 128, N)
+        np.testing.assert_array_equal(bits_u8(ys[i]).reshape(-1), eo[off * N:(off + m) * N])
+        nb = (m + 127) // 128
+        np.testing.assert_array_equal(ss[i].cpu().numpy().view(np.uint32), es[soff:soff + nb].view(np.uint32))
+        off += m
+        soff += nb
+
+
+# ------------------------------------------------------------- dual layout
+@pytest.mark.parametrize("M,K,seed", [(32, 32, 1), (64, 7168, 2), (96, 1056, 3), (256, 256, 4)])
+def test_dual_layout(oracle, dev, M, K, seed):
+    _say("dual", M, K)
+    from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4_dual
+    x = (torch.randn((M, K), generator=torch.Generator().manual_seed(seed)) * 2).to(torch.bfloat16)
+    xb = bits_u16(x)
+    xb[0, :32] = special_blocks()[32 * 6: 32 * 7]  # an inf block in row 0
+    xd = from_u16(xb, dev)
+    rq, rs, cq, cs = omo_per_token_group_quant_mxfp4_dual(xd)
+    torch.cuda.synchronize()
+    eq, es = oracle.quant_mxfp4(xb.reshape(-1))
+    np.testing.assert_array_equal(bits_u8(rq).reshape(-1), eq)
+    np.testing.assert_array_equal(bits_u8(rs).reshape(-1), es)
+    eqt, est = oracle.quant_mxfp4(np.ascontiguousarray(xb.T).reshape(-1))
+    np.testing.assert_array_equal(bits_u8(cq).reshape(-1), eqt)
+    np.testing.assert_array_equal(bits_u8(cs).reshape(-1), est)
