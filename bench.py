@@ -1,0 +1,319 @@
+#!/usr/bin/env python3
+"""Benchmark of the MXFP4 hot path on one MI355X.
+
+A step is one BF16 -> MXFP4 rowwise quantize of the 8192 x 7168 activation
+tensor (N(0,1), 0.1% of the channels x100), launched through the C ABI
+(omo_hip_per_token_group_quant_fp4) on torch's current HIP stream. Inputs are
+resident in HBM before the timed region. Four input/output buffer sets
+(594 MB) rotate so that the 256 MB Infinity Cache cannot hold the working
+set. The script prints one JSON line.
+
+Also measured (extra keys): MXFP4 -> BF16 dequant of the same shape, the
+MoE-payload requant/dequant (4096 x 7168), the dual-layout quantize
+(7168 x 18432) and the row -> col FP8 conversion, each as GB/s of
+algorithmic bytes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       [--only quant|dequant|...] [--copy-calibration]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mxfp4-hopper_amd"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published peak
+METRIC = "BF16→MXFP4 quantize GB/s & % HBM peak at 8192×7168; dequant GB/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (>= 3 to exceed the 256 MB cache)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of legs: quant,dequant,payload,dual,rowcol")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 1 GiB device copy (known traffic) for counter calibration")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="time eagerly enqueued launches only (no HIP graph), e.g. under counter collection")
+    return ap.parse_args()
+
+
+def sleep_gpu(torch, ms=5.0):
+    """Keep the GPU busy while the host enqueues the timed launches, so the
+    timed region measures the GPU rather than the host's enqueue rate."""
+    try:
+        torch.cuda._sleep(int(ms * 2.4e6))
+    except Exception:
+        pass
+
+
+GRAPH = True
+
+
+def time_launches(torch, launch, n_sets, steps, warmup, graph=None):
+    """Warm up, then time exactly `steps` back-to-back launches (rotating over
+    the buffer sets) with one HIP event at each end of the timed region, on the
+    stream the kernels run on. With graph=True the `steps` launches are first
+    captured into one HIP graph, whose single replay is the timed region.
+    Returns (total_ms, eager_total_ms)."""
+    for i in range(warmup):
+        launch(i % n_sets)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sleep_gpu(torch)
+    t0.record()
+    for i in range(steps):
+        launch(i % n_sets)
+    t1.record()
+    torch.cuda.synchronize()
+    eager = t0.elapsed_time(t1)
+    if not (GRAPH if graph is None else graph):
+        return eager, eager
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                launch(i % n_sets)
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()  # untimed warm replay
+    torch.cuda.synchronize()
+    t0.record()
+    g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    total = t0.elapsed_time(t1)
+    del g
+    return total, eager
+
+
+def main():
+    global GRAPH
+    args = parse()
+    GRAPH = not args.eager
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                          "(multi-GPU sharding is described in DESIGN.md but not built)"}))
+        sys.exit(2)
+    import torch
+    import omo
+    from omo import _abi
+    import omo_workloads as wl
+
+    lib = _abi.lib
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cur = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda leg: not only or leg in only)
+
+    if args.copy_calibration:
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device=dev)
+        b = torch.empty(n, dtype=torch.uint8, device=dev)
+        a.fill_(1)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n}))
+        return
+
+    out = {}
+    M, K = 8192, 7168
+    numel = M * K
+    qbytes = wl.quant_bytes(numel)
+
+    # ---- inputs resident in HBM: args.sets independent buffer sets
+    xs = [wl.activations_with_outliers(M, K, seed=2026 + i, device=dev) for i in range(args.sets)]
+    qs = [torch.empty((M, K // 2), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+    ss = [torch.empty((M, K // 32), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+    torch.cuda.synchronize()
+
+    def quant(i):
+        rc = lib.omo_hip_per_token_group_quant_fp4(xs[i].data_ptr(), numel, qs[i].data_ptr(), numel // 2,
+                                                   ss[i].data_ptr(), numel // 32, 32, 1e-10, -6.0, 6.0, 0, cur())
+        if rc:
+            _abi.check(rc)
+
+    total_ms, eager_ms = time_launches(torch, quant, args.sets, args.steps, args.warmup)
+    ms_step = total_ms / args.steps
+    # the timed region holds only the quantize launches, so its average
+    # launch duration is the region's duration over the launch count
+    avg_launch_ms = ms_step
+    value = qbytes / (ms_step * 1e-3) / 1e9
+    achieved = value
+    out["eager_launches"] = {"GB/s": round(qbytes / (eager_ms / args.steps * 1e-3) / 1e9, 1),
+                             "us_per_launch": round(eager_ms / args.steps * 1e3, 3),
+                             "note": "same launches enqueued one by one from Python instead of one graph replay"}
+
+    # parity of the timed outputs (set 0) against the CPU oracle, and the CPU baseline
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import numpy as np
+        import oracle
+        xb = xs[0].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+        nthreads = min(16, os.cpu_count() or 1)
+        times = []
+        t_end = time.time() + args.cpu_seconds
+        while len(times) < 3 or (time.time() < t_end and len(times) < 2000):
+            t0 = time.perf_counter()
+            eq, es = oracle.quant_mxfp4(xb, nthreads=nthreads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        parity = bool(np.array_equal(qs[0].cpu().numpy().reshape(-1), eq) and
+                      np.array_equal(ss[0].cpu().numpy().reshape(-1), es))
+        cpu = {"value": round(qbytes / med / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+               "sample": f"oracle quantize of the full 8192x7168 cfg2 tensor, {len(times)} reps, median "
+                         f"{med * 1e3:.1f} ms ({sum(times):.1f} s of CPU work)"}
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_quant_rowwise_cfg2.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    # ---- extra legs -------------------------------------------------------
+    if want("dequant"):
+        ys = [torch.empty((M, K), dtype=torch.bfloat16, device=dev) for _ in range(args.sets)]
+
+        def dequant(i):
+            rc = lib.omo_hip_per_token_Mxfp4ToBf16_dequant(qs[i].data_ptr(), numel // 2, ss[i].data_ptr(),
+                                                           numel // 32, ys[i].data_ptr(), numel, None, 0, 32,
+                                                           1e-10, -6.0, 6.0, 0, cur())
+            if rc:
+                _abi.check(rc)
+        steps = max(100, args.steps // 4)
+        t, _ = time_launches(torch, dequant, args.sets, steps, 20)
+        dq = wl.dequant_bytes(numel)
+        out["dequant"] = {"workload": "MXFP4->BF16 8192x7168", "GB/s": round(dq / (t / steps * 1e-3) / 1e9, 1),
+                          "us_per_launch": round(t / steps * 1e3, 2),
+                          "frac_of_peak": round(dq / (t / steps * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del ys
+
+    if want("payload"):
+        # cfg4: one GPU's share of the MoE dispatch payload, requant to FP8 and dequant to bf16
+        Mp = 4096
+        n4 = Mp * K
+        x4 = wl.normal_bf16((Mp, K), seed=44, device=dev)
+        q4 = [torch.empty((Mp, K // 2), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+        s4 = [torch.empty((Mp, K // 32), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+        for i in range(args.sets):
+            omo.omo_per_token_group_quant_fp4(x4, q4[i], s4[i], 32, 1e-10, -6.0, 6.0, False)
+        f8 = [torch.empty((Mp, K), dtype=torch.float8_e4m3fn, device=dev) for _ in range(args.sets)]
+        f8s = [torch.empty((K // 128, Mp), dtype=torch.float32, device=dev) for _ in range(args.sets)]
+
+        def requant(i):
+            rc = lib.omo_hip_per_token_Mxfp4ToFp8(q4[i].data_ptr(), Mp, K // 2, s4[i].data_ptr(), n4 // 32,
+                                                  f8[i].data_ptr(), n4, f8s[i].data_ptr(), n4 // 128, 128, 1e-10,
+                                                  -6.0, 6.0, 0, cur())
+            if rc:
+                _abi.check(rc)
+        steps = max(100, args.steps // 4)
+        t, _ = time_launches(torch, requant, args.sets, steps, 20)
+        rb = wl.requant_fp8_bytes(n4)
+        out["payload_requant_fp8"] = {"workload": "MXFP4->FP8 E4M3 1x128 4096x7168",
+                                      "kernel_GB/s": round(rb / (t / steps * 1e-3) / 1e9, 1),
+                                      "us_per_launch": round(t / steps * 1e3, 2)}
+        y4 = [torch.empty((Mp, K), dtype=torch.bfloat16, device=dev) for _ in range(args.sets)]
+
+        def deq4(i):
+            rc = lib.omo_hip_per_token_Mxfp4ToBf16_dequant(q4[i].data_ptr(), n4 // 2, s4[i].data_ptr(), n4 // 32,
+                                                           y4[i].data_ptr(), n4, None, 0, 32, 1e-10, -6.0, 6.0, 0,
+                                                           cur())
+            if rc:
+                _abi.check(rc)
+        t, _ = time_launches(torch, deq4, args.sets, steps, 20)
+        db = wl.dequant_bytes(n4)
+        out["payload_dequant_bf16"] = {"workload": "MXFP4->BF16 4096x7168",
+                                       "kernel_GB/s": round(db / (t / steps * 1e-3) / 1e9, 1),
+                                       "us_per_launch": round(t / steps * 1e3, 2)}
+        del q4, s4, f8, f8s, y4, x4
+
+    if want("dual"):
+        Mw, Kw = 7168, 18432
+        nw = Mw * Kw
+        sets = 2  # 2 x 404 MB exceeds the 256 MB cache
+        xw = [wl.heavy_tail_weights(Mw, Kw, seed=33 + i, device=dev) for i in range(sets)]
+        rq = [torch.empty((Mw, Kw // 2), dtype=torch.uint8, device=dev) for _ in range(sets)]
+        rs = [torch.empty((Mw, Kw // 32), dtype=torch.uint8, device=dev) for _ in range(sets)]
+        cq = [torch.empty((Kw, Mw // 2), dtype=torch.uint8, device=dev) for _ in range(sets)]
+        cs = [torch.empty((Kw, Mw // 32), dtype=torch.uint8, device=dev) for _ in range(sets)]
+
+        def dual(i):
+            rc = lib.omo_hip_quant_mxfp4_dual(xw[i].data_ptr(), Mw, Kw, rq[i].data_ptr(), nw // 2, rs[i].data_ptr(),
+                                              nw // 32, cq[i].data_ptr(), nw // 2, cs[i].data_ptr(), nw // 32, 1e-10,
+                                              cur())
+            if rc:
+                _abi.check(rc)
+        steps = max(50, args.steps // 10)
+        t, _ = time_launches(torch, dual, sets, steps, 10)
+        b = wl.dual_quant_bytes(nw)
+        out["dual_quant"] = {"workload": "rowwise+columnwise MXFP4 7168x18432",
+                             "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
+                             "us_per_launch": round(t / steps * 1e3, 2)}
+        del xw, rq, rs, cq, cs
+
+    if want("rowcol"):
+        Mr, Nr = 4096, 7168
+        q5 = [torch.empty((Mr, Nr // 2), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+        s5 = [torch.empty((Mr, Nr // 32), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+        x5 = wl.normal_bf16((Mr, Nr), seed=55, device=dev)
+        for i in range(args.sets):
+            omo.omo_per_token_group_quant_fp4(x5, q5[i], s5[i], 32, 1e-10, -6.0, 6.0, False)
+        o5 = [torch.empty((Nr, Mr), dtype=torch.float8_e4m3fn, device=dev) for _ in range(args.sets)]
+        os5 = [torch.empty((Mr // 128, Nr), dtype=torch.float32, device=dev) for _ in range(args.sets)]
+
+        def rowcol(i):
+            rc = lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(q5[i].data_ptr(), Mr, Nr // 2, s5[i].data_ptr(), Mr,
+                                                              Nr // 32, o5[i].data_ptr(), Nr, Mr, os5[i].data_ptr(),
+                                                              Mr // 128, Nr, 1e-10, cur())
+            if rc:
+                _abi.check(rc)
+        steps = max(100, args.steps // 4)
+        t, _ = time_launches(torch, rowcol, args.sets, steps, 20)
+        b = wl.row_to_col_fp8_bytes(Mr, Nr)
+        out["row_to_col_fp8"] = {"workload": "MXFP4 rowwise -> FP8 columnwise 4096x7168",
+                                 "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
+                                 "us_per_launch": round(t / steps * 1e3, 2)}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2 per-token BF16->MXFP4 quantize, 8192x7168, N(0,1) with 0.1% of channels "
+                               "x100, rowwise 1x32 E2M1 + E8M0", "rows": M, "cols": K,
+                   "algorithmic_bytes_per_step": qbytes, "buffer_sets": args.sets},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "quant_rowwise_kernel", "avg_launch_us": round(avg_launch_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "parity_vs_oracle": parity,
+        "timing": "eager launches" if args.eager else "one HIP-graph replay of the timed launches",
+    }
+    line.update(out)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+"""CPU-only checks of the boundary: the C ABI library loads and exports every
+function declared in include/omo_mxfp4.h, argument validation runs (and
+fails correctly) before any HIP call, and the Python layers apply the
+reference's host checks. No call here reaches a kernel launch.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "omo_mxfp4.h")).read()
+    return re.findall(r"OMO_API\s+(?:const\s+)?\w+\*?\s+(omo_hip_\w+)\s*\(", text)
+
+
+def test_header_declares_the_reference_entry_points():
+    names = set(declared_symbols())
+    for n in ["omo_hip_per_token_group_quant_fp4", "omo_hip_per_token_Mxfp4ToBf16_dequant",
+              "omo_hip_per_token_Mxfp4ToFp8", "omo_hip_per_token_Mxfp4ToBf16ToFp8",
+              "omo_hip_per_token_Mxfp4ToFp8_col", "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col",
+              "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit", "omo_hip_quant_mxfp4_dual",
+              "omo_hip_abi_version", "omo_hip_status_string", "omo_hip_last_error"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from omo import _abi
+    lib = ctypes.CDLL(_abi.LIB_PATH)
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert _abi.lib.omo_hip_abi_version() == 1
+    assert _abi.lib.omo_hip_status_string(-1) == b"invalid argument"
+
+
+def _lib():
+    from omo import _abi
+    return _abi.lib
+
+
+def test_quant_validation_paths():
+    lib = _lib()
+    P = ctypes.c_void_p
+    fake = P(0x1000)  # never dereferenced: every call below fails validation
+    # numel % group_size
+    assert lib.omo_hip_per_token_group_quant_fp4(fake, 40, fake, 20, fake, 1, 32, 1e-10, -6.0, 6.0, 0, None) == -1
+    assert b"group_size" in lib.omo_hip_last_error()
+    # unsupported modes
+    assert lib.omo_hip_per_token_group_quant_fp4(fake, 64, fake, 32, fake, 2, 32, 1e-10, -6.0, 6.0, 1, None) == -2
+    assert lib.omo_hip_per_token_group_quant_fp4(fake, 128, fake, 64, fake, 2, 64, 1e-10, -6.0, 6.0, 0, None) == -2
+    # undersized outputs, null pointers, misalignment, bad constants
+    assert lib.omo_hip_per_token_group_quant_fp4(fake, 64, fake, 31, fake, 2, 32, 1e-10, -6.0, 6.0, 0, None) == -1
+    assert lib.omo_hip_per_token_group_quant_fp4(None, 64, fake, 32, fake, 2, 32, 1e-10, -6.0, 6.0, 0, None) == -1
+    assert lib.omo_hip_per_token_group_quant_fp4(P(0x1002), 64, fake, 32, fake, 2, 32, 1e-10, -6.0, 6.0, 0, None) == -1
+    assert lib.omo_hip_per_token_group_quant_fp4(fake, 64, fake, 32, fake, 2, 32, float("nan"), -6.0, 6.0, 0,
+                                                 None) == -1
+    assert lib.omo_hip_per_token_group_quant_fp4(fake, 64, fake, 32, fake, 2, 32, 1e-10, -6.0, 0.0, 0, None) == -1
+    # empty input is a no-op success
+    assert lib.omo_hip_per_token_group_quant_fp4(None, 0, None, 0, None, 0, 32, 1e-10, -6.0, 6.0, 0, None) == 0
+
+
+def test_requant_validation_paths():
+    lib = _lib()
+    f = ctypes.c_void_p(0x1000)
+    # dequant: numel % 128
+    assert lib.omo_hip_per_token_Mxfp4ToBf16_dequant(f, 64, f, 4, f, 128, None, 0, 32, 1e-10, -6.0, 6.0, 0,
+                                                     None) == -1
+    # rowwise fp8: row bytes % 64, numel % 128
+    assert lib.omo_hip_per_token_Mxfp4ToFp8(f, 4, 32, f, 8, f, 256, f, 2, 128, 1e-10, -6.0, 6.0, 0, None) == -1
+    assert lib.omo_hip_per_token_Mxfp4ToFp8(f, 3, 64, f, 12, f, 384, f, 3, 128, 1e-10, -6.0, 6.0, 0, None) == -1
+    assert lib.omo_hip_per_token_Mxfp4ToBf16ToFp8(f, 2, 64, f, 8, f, 255, f, 2, 128, 1e-10, -6.0, 6.0, 0,
+                                                  None) == -1
+    # col: whole 128x128-byte tiles only
+    assert lib.omo_hip_per_token_Mxfp4ToFp8_col(f, 64, 128, f, 512, f, 16384, f, 128, 128, 1e-10, -6.0, 6.0, 0,
+                                                None) == -1
+    # row->col: the reference's shape checks
+    assert lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(f, 4, 32, f, 4, 1, f, 64, 4, f, 1, 64, 1e-10, None) == -1
+    assert lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(f, 4, 32, f, 4, 2, f, 4, 64, f, 1, 64, 1e-10, None) == -1
+    # msplit: output too small
+    assert lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(f, 4, 32, f, 8, f, 100, f, 64, f, f, f, 1, 4,
+                                                               1e-10, None) == -1
+    # dual: multiples of 32
+    assert lib.omo_hip_quant_mxfp4_dual(f, 48, 32, f, 768, f, 48, f, 768, f, 48, 1e-10, None) == -1
+
+
+def test_omo_binding_host_checks():
+    import omo
+    x = torch.zeros((2, 64), dtype=torch.bfloat16)
+    q = torch.zeros((2, 32), dtype=torch.uint8)
+    s = torch.zeros((2, 2), dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        omo.omo_per_token_group_quant_fp4(x, q, s, 32, 1e-10, -6.0, 6.0, False)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        omo.omo_per_token_Mxfp4ToBf16_dequant(q, s, x, torch.zeros(1, 1), 32, 1e-10, -6.0, 6.0, False)
+    with pytest.raises(NotImplementedError):
+        omo.omo_per_token_group_quant_fp4_fused_ToFp8(x, q, s, x, s, 32, 1e-10, -6.0, 6.0, False)
+    # keyword names of the reference binding (code/kernel/ops.cu:28-41)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        omo.omo_per_token_group_quant_fp4(input=x, output_q=q, output_s=s, group_size=32, eps=1e-10, fp4_min=-6.0,
+                                          fp4_max=6.0, scale_ue8m0=False)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        omo.omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(input=q, input_s=s, output_q=q, output_s=s, m_splits=s,
+                                                        split_offsets=s, scale_offsets=s, max_split_len=2, eps=1e-10)
+
+
+def test_wrapper_host_helpers():
+    from omo_python_api.mxfp4_dequant import pad_to_multiple, split_metadata, unpad_from_multiple
+    x = torch.arange(2 * 70, dtype=torch.uint8).view(2, 70)
+    p, w = pad_to_multiple(x, 64)
+    assert p.shape == (2, 128) and w == 70 and torch.equal(p[:, :70], x) and int(p[:, 70:].sum()) == 0
+    same, w2 = pad_to_multiple(x[:, :64].contiguous(), 64)
+    assert same.shape == (2, 64) and w2 == 64
+    assert unpad_from_multiple(p, 70).shape == (2, 70)
+    lens, offs, soffs, mx, rows, srows = split_metadata([1, 127, 0, 128, 300], "cpu")
+    assert lens.tolist() == [1, 127, 0, 128, 300]
+    assert offs.tolist() == [0, 1, 128, 128, 256]
+    assert soffs.tolist() == [0, 1, 2, 2, 3]
+    assert (mx, rows, srows) == (300, 556, 6)
+    assert lens.dtype == torch.int32
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "exactly one GPU" in r.stdout

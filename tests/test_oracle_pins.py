@@ -1,0 +1,322 @@
+"""Pins of the CPU oracle against independent statements of the mathematics.
+
+The reference ships no tests or golden vectors, so each oracle function is
+checked against something that does not share its code path:
+  * E8M0 scale rule  -> exact ceil(log2(amax/6)) by integer comparison, all
+                        65,536 bf16 amax values, plus hand-derived values;
+  * E2M1 rounding    -> textbook round-to-nearest-even onto the E2M1 grid in
+                        float64, every bf16 value under every reachable scale;
+  * dequant          -> exact products code * 2^(s-127) cast by torch to bf16;
+  * FP8 E4M3         -> torch's float8_e4m3fn cast;
+  * requant layouts  -> exact values placed by numpy reshapes / transposes;
+  * invariants       -> value idempotence of quantize o dequantize and the
+                        half-step error bound.
+A plausible mistake in the oracle (an off-by-one exponent, a floor for a
+ceil, ties away from zero, a transposed index) fails at least one of these.
+"""
+import numpy as np
+import pytest
+import torch
+
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def bf16_values(bits):
+    with np.errstate(invalid="ignore"):
+        return (np.asarray(bits, np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def textbook_e2m1(q):
+    """Round-to-nearest-even onto {0, .5, 1, 1.5, 2, 3, 4, 6}, saturating at
+    6, sign kept (negative zero -> 0x8). q: finite float64."""
+    sign = np.signbit(q).astype(np.uint8) << 3
+    a = np.minimum(np.abs(q), 6.0)
+    hi = np.clip(np.searchsorted(E2M1, a), 1, 7)
+    lo = hi - 1
+    dlo, dhi = a - E2M1[lo], E2M1[hi] - a
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo)
+    return (sign | code).astype(np.uint8)
+
+
+def exact_ceil_log2_ratio(a, d=6.0):
+    """Smallest integer k with d * 2^k >= a, for finite a > 0 (float64 exact:
+    d * 2^k is exact and the comparison is exact)."""
+    k = np.ceil(np.log2(a / d)).astype(np.int64)
+    k = np.where(d * np.exp2(k - 1.0) >= a, k - 1, k)
+    k = np.where(d * np.exp2(k * 1.0) < a, k + 1, k)
+    return k
+
+
+def nibbles(codes):
+    c = np.asarray(codes, np.uint8)
+    out = np.empty(c.size * 2, np.uint8)
+    out[0::2] = c & 0xF
+    out[1::2] = c >> 4
+    return out
+
+
+# ------------------------------------------------------------------ E8M0
+def test_e8m0_scale_all_bf16_amax(oracle):
+    bits = np.arange(65536, dtype=np.uint32)
+    blocks = np.zeros((65536, 32), np.uint16)
+    blocks[:, 0] = bits
+    _, s = oracle.quant_mxfp4(blocks.reshape(-1))
+    v = np.abs(bf16_values(bits))
+    finite = np.isfinite(v)
+    eps = np.float64(np.float32(1e-10))
+    amax = np.where(finite & (v > eps), v, eps)  # NaN ignored, eps floor
+    k = np.maximum(exact_ceil_log2_ratio(amax), -33)
+    expected = (k + 127).astype(np.uint8)
+    expected[np.isinf(v)] = 126  # y_s = inf, (int)log2f(inf) saturates, +127 wraps
+    np.testing.assert_array_equal(s, expected)
+    # the OCP-style floor(log2 amax) - 2 rule differs on a large share of values
+    norm = finite & (v > 1e-9)
+    ocp = np.floor(np.log2(v[norm])).astype(np.int64) - 2 + 127
+    assert np.mean(ocp != expected[norm]) > 0.2
+
+
+@pytest.mark.parametrize("amax,byte", [(6.0, 127), (3.0, 126), (1.0, 125), (6.03125, 128), (0.0, 94),
+                                       (float("inf"), 126), (1.5 * 2.0 ** 127, 252), (3.3895313892515355e38, 253)])
+def test_e8m0_known_answers(oracle, amax, byte):
+    x = torch.zeros(32, dtype=torch.float32)
+    x[3] = amax
+    xb = x.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    _, s = oracle.quant_mxfp4(xb)
+    assert s[0] == byte
+
+
+# ------------------------------------------------------------------ E2M1
+def domain_blocks():
+    vals, cs = [], []
+    for c in range(-33, 127):
+        anchor = 0x7F7F if c == 126 else 0x40C0 + (c << 7)
+        mags = np.arange(anchor + 1, dtype=np.uint32)
+        v = np.concatenate([mags, mags | 0x8000]).astype(np.uint16)
+        nblk = -(-v.size // 31)
+        pad = np.zeros(nblk * 31, np.uint16)
+        pad[: v.size] = v
+        blk = np.empty((nblk, 32), np.uint16)
+        blk[:, 0] = anchor
+        blk[:, 1:] = pad.reshape(nblk, 31)
+        vals.append(blk.reshape(-1))
+        cs.append(np.full(nblk * 32, c, np.int64))
+    return np.concatenate(vals), np.concatenate(cs)
+
+
+def test_e2m1_textbook_rne_full_domain(oracle):
+    xb, c = domain_blocks()
+    q, s = oracle.quant_mxfp4(xb)
+    np.testing.assert_array_equal(s, (c[::32] + 127).astype(np.uint8))
+    x = bf16_values(xb)
+    expected = textbook_e2m1(x / np.exp2(c.astype(np.float64)))
+    np.testing.assert_array_equal(nibbles(q), expected)
+
+
+@pytest.mark.parametrize("q,code", [(0.25, 0x0), (0.2500001, 0x0), (0.26, 0x1), (0.75, 0x2), (1.25, 0x2),
+                                    (1.75, 0x4), (2.5, 0x4), (3.5, 0x6), (5.0, 0x6), (5.5, 0x7), (6.0, 0x7),
+                                    (-0.0, 0x8), (-0.3, 0x9), (-6.0, 0xF), (2.0 ** -94, 0x0), (2.0 ** -95, 0x0)])
+def test_e2m1_known_answers(oracle, q, code):
+    # 0.2500001 is not a bf16 product; the reference's shift drops its low
+    # mantissa bits, so it rounds like 0.25 (the test records that behaviour).
+    assert oracle.e2m1_from_f32(q) == code
+
+
+def test_quant_special_values_known_answers(oracle):
+    inf, nan = 0x7F80, 0x7FC0
+    one = 0x3F80
+    blk = np.zeros((5, 32), np.uint16)
+    blk[0, :] = 0                                   # zero block
+    blk[1, :] = [nan] + [one] * 31                  # NaN ignored by amax; NaN -> -6
+    blk[2, :] = [inf, 0xFF80, one, 0xBF80] + [0] * 28  # inf block
+    blk[3, :] = [0x8000, 0x0001, 0x8001] + [0] * 29  # -0 and denormals
+    blk[4, :] = [0x40C0, 0x3F00, 0xC0C0, 0x3F40] + [0] * 28
+    q, s = oracle.quant_mxfp4(blk.reshape(-1))
+    n = nibbles(q).reshape(5, 32)
+    assert list(s) == [94, 125, 126, 94, 127]
+    assert n[0].tolist() == [0] * 32
+    assert n[1, 0] == 0xF and n[1, 1] == 0x6  # 1.0 at scale 2^-2 -> 4.0 (code 6)
+    assert n[2, :4].tolist() == [0xF, 0xF, 0x0, 0x8]
+    assert n[3, :3].tolist() == [0x8, 0x0, 0x8]
+    assert n[4, :4].tolist() == [0x7, 0x1, 0xF, 0x2]
+    assert q[0 * 16] == 0 and q[4 * 16] == 0x17 and q[4 * 16 + 1] == 0x2F
+
+
+# --------------------------------------------------------------- dequant
+def e2m1_signed(n):
+    v = E2M1[n & 7]
+    return np.where(n & 8, -v, v)
+
+
+def test_dequant_all_bytes_all_scales(oracle):
+    q = np.tile(np.arange(256, dtype=np.uint8), 256)
+    s = np.repeat(np.arange(256, dtype=np.uint8), 16)
+    got = oracle.dequant_bf16(q, s)
+    n = nibbles(q).astype(np.int64)
+    sb = np.repeat(s, 32).astype(np.int64)
+    val = e2m1_signed(n)
+    neg = (n & 8) != 0
+    with np.errstate(invalid="ignore", over="ignore"):
+        scale = np.where(sb == 0, 0.0, np.where(sb == 255, np.inf, np.exp2(sb - 127.0)))
+        exact = val * scale
+        # -0 * scale keeps the sign; 0 * inf is NaN
+        exact = np.where((val == 0) & (sb != 255), np.where(neg, -0.0, 0.0), exact)
+    t = torch.from_numpy(exact.astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    isnan = np.isnan(exact)
+    np.testing.assert_array_equal(got[~isnan], t[~isnan])
+    assert np.all(got[isnan] == 0x7FFF)
+    # known answer: byte 0x72 at scale 127 -> (1.0, 6.0)
+    assert oracle.dequant_bf16(np.array([0x72] + [0] * 127, np.uint8), np.full(8, 127, np.uint8))[:2].tolist() == \
+        [0x3F80, 0x40C0]
+
+
+def test_quant_dequant_value_idempotence_and_error_bound(oracle):
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn((512, 1024), generator=g) * torch.logspace(-20, 20, 1024)).to(torch.bfloat16)
+    xb = x.view(torch.int16).numpy().view(np.uint16).reshape(-1)
+    q, s = oracle.quant_mxfp4(xb)
+    y = oracle.dequant_bf16(q, s)
+    q2, s2 = oracle.quant_mxfp4(y)
+    y2 = oracle.dequant_bf16(q2, s2)
+    np.testing.assert_array_equal(y, y2)
+    # |dq(q(x)) - x| <= half the E2M1 step at the block scale (step 2 at |q| in [4, 6])
+    xv = bf16_values(xb)
+    yv = bf16_values(y)
+    scale = np.exp2(np.repeat(s.astype(np.float64) - 127, 32))
+    err = np.abs(yv - xv) / scale
+    qa = np.abs(xv) / scale
+    step = np.where(qa < 2, 0.5, np.where(qa < 4, 1.0, 2.0))
+    assert np.all(err <= step / 2 + 1e-12)
+
+
+# ------------------------------------------------------------------ FP8
+def test_e4m3_conversion_matches_torch(oracle):
+    bits = np.arange(65536, dtype=np.uint32)
+    f = (bits << 16).view(np.float32)
+    rng = np.random.default_rng(0)
+    r = rng.uniform(-448, 448, 20000).astype(np.float32)
+    # midpoints between neighbouring E4M3 values and their float neighbours
+    grid = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    grid = np.unique(grid[np.isfinite(grid)])
+    mids = ((grid[1:] + grid[:-1]) / 2).astype(np.float32)
+    cand = np.concatenate([f, r, mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, -np.float32(np.inf))])
+    cand = cand[np.isfinite(cand) & (np.abs(cand) <= 448)]
+    exp = torch.from_numpy(cand).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = np.array([oracle.f32_to_e4m3(float(v)) for v in cand], np.uint8)
+    np.testing.assert_array_equal(got, exp)
+
+
+def fp8_of(values):
+    return torch.from_numpy(np.clip(values, -448, 448).astype(np.float32)).to(torch.float8_e4m3fn) \
+        .view(torch.uint8).numpy()
+
+
+def test_to_fp8_rowwise_exact_values(oracle):
+    rng = np.random.default_rng(1)
+    M, Kb = 64, 256
+    q = rng.integers(0, 256, size=(M, Kb), dtype=np.uint8)
+    base = rng.integers(10, 250, size=(M, Kb // 64, 1))
+    s = (base - rng.integers(0, 6, size=(M, Kb // 64, 4))).astype(np.uint8)  # within 6 of the group max
+    out, outs = oracle.mxfp4_to_fp8(q, s.reshape(M, -1))
+    smax = s.max(axis=2)
+    n = nibbles(q.reshape(-1)).astype(np.int64).reshape(M, Kb // 64, 128)
+    si = np.repeat(s, 32, axis=2).astype(np.int64)
+    exact = e2m1_signed(n) * np.exp2(si - smax[..., None] + 6.0)
+    np.testing.assert_array_equal(out.reshape(M, Kb // 64, 128), fp8_of(exact).reshape(M, Kb // 64, 128))
+    np.testing.assert_array_equal(outs, np.exp2(smax.T - 133.0).astype(np.float32))  # [K/64, M]
+
+
+def test_to_fp8_rowwise_wrap_known_answers(oracle):
+    M, Kb = 1, 64
+    q = np.zeros((M, Kb), np.uint8)
+    q[0, 16:] = 0x22  # 1.0 codes in blocks 1..3
+    s = np.array([[120, 127, 127, 127]], np.uint8)  # block 0 is 7 below max: zero codes wrap
+    out, outs = oracle.mxfp4_to_fp8(q, s)
+    assert np.all(out[0, :32] == 0xFE)     # zero code, s_i = max - 7 -> -inf -> -448
+    assert np.all(out[0, 32:] == 0x68)     # 1.0 * 2^6 = 64 = E4M3 0x68
+    q2 = np.full((1, 64), 0x22, np.uint8)
+    out2, outs2 = oracle.mxfp4_to_fp8(q2, np.array([[5, 5, 5, 5]], np.uint8))
+    assert np.isinf(outs2[0, 0])           # max < 6 wraps: (uint8)(5 - 6) = 255 -> inf
+    assert np.all(out2 == 0x68)
+
+
+def test_to_fp8_col_exact_values_and_layout(oracle):
+    rng = np.random.default_rng(2)
+    M, Kb = 256, 256
+    q = rng.integers(0, 256, size=(M, Kb), dtype=np.uint8)
+    q[(q & 0x07) == 0] |= 0x01
+    q[(q & 0x70) == 0] |= 0x10  # no +-0 nibbles: zero codes wrap (checked below)
+    s = rng.integers(100, 110, size=(M, Kb // 16)).astype(np.uint8)
+    out, outs = oracle.mxfp4_to_fp8_col(q, s)
+    n = nibbles(q.reshape(-1)).astype(np.int64).reshape(M, 2 * Kb)
+    mt = s.reshape(M // 128, 128, Kb // 16).max(axis=1)           # [M/128, MX cols]
+    g = np.repeat(mt.astype(np.int64) - 6, 128, axis=0)          # per row
+    g = np.repeat(g, 32, axis=1)                                  # per element
+    si = np.repeat(s.astype(np.int64), 32, axis=1)
+    exact = np.abs(e2m1_signed(n)) * np.exp2(si - g)             # sign dropped
+    np.testing.assert_array_equal(out, fp8_of(exact).reshape(M, 2 * Kb).T)
+    np.testing.assert_array_equal(outs, np.repeat(np.exp2(mt - 6.0 - 127), 32, axis=1).astype(np.float32))
+    # zero code with g - s >= 1 -> +inf -> 448
+    q0 = np.zeros((128, 128), np.uint8)
+    s0 = np.full((128, 8), 100, np.uint8)
+    s0[0, 0] = 120
+    o0, _ = oracle.mxfp4_to_fp8_col(q0, s0)
+    assert o0[0, 1] == 0x7E and o0[0, 0] == 0x00
+    q0[1, 0] = 0x88  # -0 codes wrap the same way once the sign is dropped
+    o1, _ = oracle.mxfp4_to_fp8_col(q0, s0)
+    assert o1[0, 1] == 0x7E and o1[1, 1] == 0x7E
+
+
+def dequant_matrix(q, s, N):
+    M = q.shape[0]
+    n = nibbles(q.reshape(-1)).reshape(M, N).astype(np.int64)
+    sc = np.repeat(s.astype(np.int64), 32, axis=1)[:, :N]
+    return (e2m1_signed(n) * np.exp2(sc - 127.0)).astype(np.float32)
+
+
+def test_row_to_fp8_col_numpy_restatement(oracle):
+    rng = np.random.default_rng(3)
+    M, N = 300, 512
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(100, 140, size=(M, N // 32)).astype(np.uint8)
+    out, outs = oracle.row_to_fp8_col(q, s, eps=1e-10)
+    V = dequant_matrix(q, s, N)
+    eps = np.float32(1e-10)
+    for t in range((M + 127) // 128):
+        tile = V[t * 128:(t + 1) * 128]
+        amax = np.maximum(eps, np.abs(tile).max(axis=0)).astype(np.float32)
+        np.testing.assert_array_equal(outs[t], (amax / np.float32(448)).astype(np.float32))
+        mult = np.where(amax > np.float32(1e-9), np.float32(448) / amax, np.float32(0)).astype(np.float32)
+        qv = (tile * mult[None, :]).astype(np.float32)
+        np.testing.assert_array_equal(out[:, t * 128:(t + 1) * 128], fp8_of(qv).reshape(tile.shape).T)
+
+
+def test_msplit_numpy_restatement(oracle):
+    rng = np.random.default_rng(4)
+    splits = [1, 127, 0, 128, 300]
+    M, N = sum(splits), 256
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(100, 140, size=(M, N // 32)).astype(np.uint8)
+    out, outs = oracle.row_to_fp8_col_msplit(q, s, splits)
+    V = dequant_matrix(q, s, N)
+    off = soff = 0
+    for m in splits:
+        blk = np.zeros((N, m), np.uint8)
+        for t in range((m + 127) // 128):
+            tile = V[off + t * 128: off + min(m, (t + 1) * 128)]
+            amax = np.abs(tile).max(axis=0)
+            k = np.ceil(np.log2(amax.astype(np.float64) / 448.0))
+            mult = np.where(amax <= 1e-10, 1.0, np.exp2(-k)).astype(np.float32)
+            np.testing.assert_array_equal(outs[soff + t], (1.0 / mult).astype(np.float32))
+            blk[:, t * 128: t * 128 + tile.shape[0]] = fp8_of(tile * mult[None, :]).reshape(tile.shape).T
+        np.testing.assert_array_equal(out[off * N:(off + m) * N].reshape(N, m), blk)
+        off += m
+        soff += (m + 127) // 128
+
+
+def test_te_pow2_scale_known_answers(oracle):
+    assert oracle.te_pow2_scale(448.0) == 1.0
+    assert oracle.te_pow2_scale(449.0) == 0.5
+    assert oracle.te_pow2_scale(1e-11) == 1.0
+    assert oracle.te_pow2_scale(1.0) == 2.0 ** 8   # 1/448 -> 2^-8 after rounding up
+    assert oracle.te_pow2_scale(float("inf")) == 0.0
