@@ -102,7 +102,7 @@ def main():
     GRAPH = not args.eager
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                          "(multi-GPU sharding is described in DESIGN.md but not built)"}))
+                          "(the path shards by rows with no exchange; only one GPU is used here)"}))
         sys.exit(2)
     import torch
     import omo
