@@ -58,6 +58,12 @@ def sleep_gpu(torch, ms=5.0):
 GRAPH = True
 
 
+def sets_for(bytes_per_set, minimum):
+    """Buffer sets to rotate so the working set exceeds 512 MB, twice the
+    256 MB Infinity Cache."""
+    return max(minimum, -(-512_000_000 // bytes_per_set))
+
+
 def time_launches(torch, launch, n_sets, steps, warmup, graph=None):
     """Warm up, then time exactly `steps` back-to-back launches (rotating over
     the buffer sets) with one HIP event at each end of the timed region, on the
@@ -206,13 +212,14 @@ def main():
         # cfg4: one GPU's share of the MoE dispatch payload, requant to FP8 and dequant to bf16
         Mp = 4096
         n4 = Mp * K
+        ps = sets_for(wl.requant_fp8_bytes(n4), args.sets)
         x4 = wl.normal_bf16((Mp, K), seed=44, device=dev)
-        q4 = [torch.empty((Mp, K // 2), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
-        s4 = [torch.empty((Mp, K // 32), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
-        for i in range(args.sets):
+        q4 = [torch.empty((Mp, K // 2), dtype=torch.uint8, device=dev) for _ in range(ps)]
+        s4 = [torch.empty((Mp, K // 32), dtype=torch.uint8, device=dev) for _ in range(ps)]
+        for i in range(ps):
             omo.omo_per_token_group_quant_fp4(x4, q4[i], s4[i], 32, 1e-10, -6.0, 6.0, False)
-        f8 = [torch.empty((Mp, K), dtype=torch.float8_e4m3fn, device=dev) for _ in range(args.sets)]
-        f8s = [torch.empty((K // 128, Mp), dtype=torch.float32, device=dev) for _ in range(args.sets)]
+        f8 = [torch.empty((Mp, K), dtype=torch.float8_e4m3fn, device=dev) for _ in range(ps)]
+        f8s = [torch.empty((K // 128, Mp), dtype=torch.float32, device=dev) for _ in range(ps)]
 
         def requant(i):
             rc = lib.omo_hip_per_token_Mxfp4ToFp8(q4[i].data_ptr(), Mp, K // 2, s4[i].data_ptr(), n4 // 32,
@@ -221,12 +228,12 @@ def main():
             if rc:
                 _abi.check(rc)
         steps = max(100, args.steps // 4)
-        t, _ = time_launches(torch, requant, args.sets, steps, 20)
+        t, _ = time_launches(torch, requant, ps, steps, 20)
         rb = wl.requant_fp8_bytes(n4)
         out["payload_requant_fp8"] = {"workload": "MXFP4->FP8 E4M3 1x128 4096x7168",
                                       "kernel_GB/s": round(rb / (t / steps * 1e-3) / 1e9, 1),
                                       "us_per_launch": round(t / steps * 1e3, 2)}
-        y4 = [torch.empty((Mp, K), dtype=torch.bfloat16, device=dev) for _ in range(args.sets)]
+        y4 = [torch.empty((Mp, K), dtype=torch.bfloat16, device=dev) for _ in range(ps)]
 
         def deq4(i):
             rc = lib.omo_hip_per_token_Mxfp4ToBf16_dequant(q4[i].data_ptr(), n4 // 2, s4[i].data_ptr(), n4 // 32,
@@ -234,7 +241,7 @@ def main():
                                                            cur())
             if rc:
                 _abi.check(rc)
-        t, _ = time_launches(torch, deq4, args.sets, steps, 20)
+        t, _ = time_launches(torch, deq4, ps, steps, 20)
         db = wl.dequant_bytes(n4)
         out["payload_dequant_bf16"] = {"workload": "MXFP4->BF16 4096x7168",
                                        "kernel_GB/s": round(db / (t / steps * 1e-3) / 1e9, 1),
@@ -267,13 +274,14 @@ def main():
 
     if want("rowcol"):
         Mr, Nr = 4096, 7168
-        q5 = [torch.empty((Mr, Nr // 2), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
-        s5 = [torch.empty((Mr, Nr // 32), dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+        rs_ = sets_for(wl.row_to_col_fp8_bytes(Mr, Nr), args.sets)
+        q5 = [torch.empty((Mr, Nr // 2), dtype=torch.uint8, device=dev) for _ in range(rs_)]
+        s5 = [torch.empty((Mr, Nr // 32), dtype=torch.uint8, device=dev) for _ in range(rs_)]
         x5 = wl.normal_bf16((Mr, Nr), seed=55, device=dev)
-        for i in range(args.sets):
+        for i in range(rs_):
             omo.omo_per_token_group_quant_fp4(x5, q5[i], s5[i], 32, 1e-10, -6.0, 6.0, False)
-        o5 = [torch.empty((Nr, Mr), dtype=torch.float8_e4m3fn, device=dev) for _ in range(args.sets)]
-        os5 = [torch.empty((Mr // 128, Nr), dtype=torch.float32, device=dev) for _ in range(args.sets)]
+        o5 = [torch.empty((Nr, Mr), dtype=torch.float8_e4m3fn, device=dev) for _ in range(rs_)]
+        os5 = [torch.empty((Mr // 128, Nr), dtype=torch.float32, device=dev) for _ in range(rs_)]
 
         def rowcol(i):
             rc = lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(q5[i].data_ptr(), Mr, Nr // 2, s5[i].data_ptr(), Mr,
@@ -282,7 +290,7 @@ def main():
             if rc:
                 _abi.check(rc)
         steps = max(100, args.steps // 4)
-        t, _ = time_launches(torch, rowcol, args.sets, steps, 20)
+        t, _ = time_launches(torch, rowcol, rs_, steps, 20)
         b = wl.row_to_col_fp8_bytes(Mr, Nr)
         out["row_to_col_fp8"] = {"workload": "MXFP4 rowwise -> FP8 columnwise 4096x7168",
                                  "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),

@@ -73,9 +73,9 @@ OMO_API int omo_hip_per_token_Mxfp4ToBf16_dequant(const void* input, int64_t inp
  * Replaces omo::omo_per_token_Mxfp4ToFp8 (code/kernel/per_token_Mxfp4ToFp8.cu:238-309,
  * declared code/kernel/per_token_Mxfp4ToFp8.h:6; imported by
  * code/kernel/api/mxfp4_dequant.py:1).
- * input: [rows, row_bytes] codes, row_bytes % 64 == 0; input_s: rows*row_bytes/16
- * bytes; output_q: [rows, 2*row_bytes] fp8 (8-byte aligned); output_s:
- * rows*row_bytes/64 floats. */
+ * input: [rows, row_bytes] codes, row_bytes % 64 == 0 (8-byte aligned); input_s:
+ * rows*row_bytes/16 bytes; output_q: [rows, 2*row_bytes] fp8 (16-byte aligned);
+ * output_s: rows*row_bytes/64 floats. */
 OMO_API int omo_hip_per_token_Mxfp4ToFp8(const void* input, int64_t rows, int64_t row_bytes, const void* input_s,
                                  int64_t input_s_bytes, void* output_q, int64_t output_q_bytes, void* output_s,
                                  int64_t output_s_elems, int group_size, float eps, float fp4_min, float fp4_max,

@@ -11,12 +11,13 @@
 // writes 16 B of bf16, so a wave reads 256 contiguous code bytes and writes
 // 1 KiB of contiguous output per instruction; 4 lanes share a scale byte.
 //
-// Fast path: for a scale byte s in [2, 252] every product code*2^(s-127) is a
-// normal bf16 value, so the result is the code's bf16 pattern with s-127
-// added to its exponent field (zero codes stay +-0). The four code-magnitude
-// patterns per exponent are looked up with v_perm_b32 from per-lane byte
-// tables that already include the exponent offset. Other scale bytes take
-// the fp32 restatement.
+// Fast path: for scale bytes 1..254, v_cvt_scalef32_pk_bf16_fp4 (two
+// elements per instruction, scale operand 2^(s-127)) returns exactly the
+// reference's rounded products, including subnormal results at s = 1 and
+// overflow to inf near s = 254; it is checked against the reference rule for
+// every code byte under every scale byte. Scale byte 0 (which the hardware
+// reads as 2^-127, the reference as 0.0) and 255 (hardware NaN, reference
+// inf) take the fp32 restatement.
 #include "omo_device.cuh"
 #include "omo_internal.h"
 
@@ -36,40 +37,20 @@ __device__ __forceinline__ u32x4 dequant_dword_ref(uint32_t c, uint32_t sb) {
   return o;
 }
 
-// Fast path, valid for 2 <= sb <= 252.
-//   mag  m = code & 7, bf16(m) = {0, 0x3F00, 0x3F80, 0x3FC0, 0x4000, 0x4040, 0x4080, 0x40C0}
-//   out  = m ? bf16(m) + (sb-127)*128 : 0, then | sign<<15.
-// Byte tables tl (low bytes) / th (high bytes) of the 8 offset patterns are
-// built once per lane; each output dword (2 elements) is two v_perm lookups.
+// Fast path, valid for 1 <= sb <= 254. Each convert's result is pinned in a
+// VGPR: ROCm 7.2 otherwise mis-assigns the halves of the bf16x2 results.
+__device__ __forceinline__ uint32_t pin_u32(uint32_t w) {
+  asm volatile("" : "+v"(w));
+  return w;
+}
+
 __device__ __forceinline__ u32x4 dequant_dword_fast(uint32_t c, uint32_t sb) {
-  const uint32_t off = ((sb - 127u) << 7) & 0xFFFFu;
-  const uint32_t off2 = off | (off << 16);
-  // Patterns for magnitudes (1,0), (3,2), (5,4), (7,6) as packed u16 pairs.
-  u16x2_t p10 = __builtin_bit_cast(u16x2_t, 0x3F000000u) + __builtin_bit_cast(u16x2_t, off2 & 0xFFFF0000u);
-  u16x2_t p32 = __builtin_bit_cast(u16x2_t, 0x3FC03F80u) + __builtin_bit_cast(u16x2_t, off2);
-  u16x2_t p54 = __builtin_bit_cast(u16x2_t, 0x40404000u) + __builtin_bit_cast(u16x2_t, off2);
-  u16x2_t p76 = __builtin_bit_cast(u16x2_t, 0x40C04080u) + __builtin_bit_cast(u16x2_t, off2);
-  const uint32_t w10 = __builtin_bit_cast(uint32_t, p10), w32 = __builtin_bit_cast(uint32_t, p32);
-  const uint32_t w54 = __builtin_bit_cast(uint32_t, p54), w76 = __builtin_bit_cast(uint32_t, p76);
-  // tl bytes [m0..m3] / [m4..m7]: low bytes of the patterns; th: high bytes.
-  const uint32_t tl_lo = __builtin_amdgcn_perm(w32, w10, 0x06040200u);
-  const uint32_t tl_hi = __builtin_amdgcn_perm(w76, w54, 0x06040200u);
-  const uint32_t th_lo = __builtin_amdgcn_perm(w32, w10, 0x07050301u);
-  const uint32_t th_hi = __builtin_amdgcn_perm(w76, w54, 0x07050301u);
+  const float sc = __uint_as_float(sb << 23);
   u32x4 o;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    // n = [byte_k & 0xF (half 0), byte_k >> 4 (half 1)]
-    uint32_t bb = __builtin_amdgcn_perm(0u, c, 0x0C000C00u | (uint32_t)(k | (k << 16)));
-    uint32_t n = (bb & 0x0000000Fu) | ((bb >> 4) & 0x000F0000u);
-    uint32_t mag = n & 0x00070007u;
-    uint32_t selL = mag | 0x0C000C00u;         // [m0, 0, m1, 0]
-    uint32_t selH = (mag << 8) | 0x000C000Cu;  // [0, m0, 0, m1]
-    uint32_t lo = __builtin_amdgcn_perm(tl_hi, tl_lo, selL);
-    uint32_t hi = __builtin_amdgcn_perm(th_hi, th_lo, selH);
-    uint32_t sign = (n & 0x00080008u) << 12;
-    o[k] = lo | hi | sign;
-  }
+  o[0] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 0)));
+  o[1] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 1)));
+  o[2] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 2)));
+  o[3] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 3)));
   return o;
 }
 
@@ -91,7 +72,7 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __res
     const int64_t i = base + (int64_t)u * 256;
     if (i >= ndw) continue;
     u32x4 o;
-    if (sb[u] - 2u <= 250u) {
+    if (sb[u] - 1u <= 253u) {
       o = dequant_dword_fast(c[u], sb[u]);
     } else {
       o = dequant_dword_ref(c[u], sb[u]);

@@ -71,8 +71,8 @@ int requant_rowwise(const char* fn, const void* input, int64_t rows, int64_t row
   REQUIRE_BUF("output_q", output_q, output_q_bytes, 2 * n);
   REQUIRE_BUF("output_s", output_s, output_s_elems, n / 64);
   REQUIRE(n / 64 < (int64_t)1 << 31, "%s: too many 128-element groups", fn);
-  REQUIRE(aligned(input, 4) && aligned(input_s, 4) && aligned(output_q, 8) && aligned(output_s, 4),
-          "%s: misaligned buffer (input/input_s need 4 B, output_q 8 B)", fn);
+  REQUIRE(aligned(input, 8) && aligned(input_s, 4) && aligned(output_q, 16) && aligned(output_s, 4),
+          "%s: misaligned buffer (input needs 8 B, input_s 4 B, output_q 16 B)", fn);
   if (n == 0) return ok();
   return from_hip(omo_hip::launch_mxfp4_to_fp8(input, input_s, output_q, static_cast<float*>(output_s), rows,
                                                row_bytes, as_stream(stream)),

@@ -27,47 +27,102 @@ namespace omo_hip {
 // Each lane converts one code dword (8 elements) into 8 FP8 bytes; 16 lanes
 // cover one group. A wave reads 256 contiguous code bytes and writes 512
 // contiguous FP8 bytes per instruction.
+//
+// The reference subtracts off = 128 * (adjust mod 512) from the bf16 pattern
+// of each code, adjust = (uint16)(g - s_i). Write d for the signed value of
+// adjust mod 512. Subtracting a multiple of 128 never touches the low 7 bits
+// and flips bit 15 exactly when the code is negative, so the result for a
+// negative code is the result for its magnitude with the sign flipped; after
+// the symmetric clamp and E4M3 rounding that is a flip of bit 7, except
+// where the pattern is a NaN (both signs clamp to +448).
+//
+// Fast path, d in [-6, 5]: code * 2^-d is a normal E4M3 value for every
+// nonzero magnitude (0.5 * 2^-5 = 2^-6 at the bottom, 6 * 2^6 = 384 at the
+// top), so its byte is the E4M3 pattern of the code with -d added to the
+// exponent field: {0x30, 0x38, 0x3C, 0x40, 0x44, 0x48, 0x4C} - 8d. A zero
+// code gives 0 for d <= 0 and the wrapped -inf -> -448 (0xFE) for d >= 1.
+// No NaN pattern arises in this range. The eight bytes form a per-lane
+// table; v_perm_b32 looks up four elements per instruction.
+__device__ __forceinline__ u32x2 to_fp8_dword_fast(uint32_t c, int d) {
+  const uint32_t sh = (uint32_t)(-8 * d);
+  // every byte stays in [0x08, 0x7C], so whole-dword arithmetic is per-byte
+  const uint32_t t_lo = (0x3C383000u + sh * 0x01010100u) | (d >= 1 ? 0xFEu : 0u);
+  const uint32_t t_hi = 0x4C484440u + sh * 0x01010101u;
+  const uint32_t lo = c & 0x0F0F0F0Fu, hi = (c >> 4) & 0x0F0F0F0Fu;
+  const uint32_t a = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // nibbles of elements 0..3
+  const uint32_t b = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // elements 4..7
+  u32x2 o;
+  o[0] = __builtin_amdgcn_perm(t_hi, t_lo, a & 0x07070707u) ^ ((a << 4) & 0x80808080u);
+  o[1] = __builtin_amdgcn_perm(t_hi, t_lo, b & 0x07070707u) ^ ((b << 4) & 0x80808080u);
+  return o;
+}
+
+// Reference restatement for one code dword under the 16-bit offset `offset`.
+__device__ __forceinline__ u32x2 to_fp8_dword_ref(uint32_t c, uint32_t offset) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t byte = (c >> (8 * k)) & 0xFFu;
+    const uint32_t a0 = (e2m1_to_bf16_bits(byte & 0xFu) - offset) & 0xFFFFu;
+    const uint32_t a1 = (e2m1_to_bf16_bits(byte >> 4) - offset) & 0xFFFFu;
+    const float f0 = fmaxf(-448.0f, fminf(448.0f, bf16_to_f32(a0)));
+    const float f1 = fmaxf(-448.0f, fminf(448.0f, bf16_to_f32(a1)));
+    const uint32_t pr = fp8x2_from_f32(f0, f1);
+    if (k < 2) lo |= pr << (16 * k); else hi |= pr << (16 * (k - 2));
+  }
+  u32x2 o;
+  o[0] = lo;
+  o[1] = hi;
+  return o;
+}
+
+// Each lane converts two code dwords (16 elements of one MX block, 8 B) into
+// 16 FP8 bytes, so loads and stores are contiguous across the wave (2 KiB
+// of codes read and 4 KiB of FP8 written per wave and step); 8 lanes cover
+// one 128-element group.
 template <int UNROLL>
-__global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint32_t* __restrict__ q,
+__global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restrict__ q,
                                                            const uint32_t* __restrict__ s4,
-                                                           u32x2* __restrict__ out, float* __restrict__ out_s,
-                                                           int64_t ndw, uint32_t M, uint32_t gpr) {
+                                                           u32x4* __restrict__ out, float* __restrict__ out_s,
+                                                           int64_t npairs, uint32_t M, uint32_t gpr) {
   const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
-  uint32_t c[UNROLL], sd[UNROLL];
+  u32x2 c[UNROLL];
+  uint32_t sd[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int64_t i = base + (int64_t)u * 256;
-    if (i < ndw) {
+    if (i < npairs) {
       c[u] = __builtin_nontemporal_load(q + i);
-      sd[u] = s4[i >> 4];
+      sd[u] = s4[i >> 3];
     }
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int64_t i = base + (int64_t)u * 256;
-    if (i >= ndw) continue;
+    if (i >= npairs) continue;
     const uint32_t s = sd[u];
     const uint32_t smax = max(max(s & 0xFFu, (s >> 8) & 0xFFu), max((s >> 16) & 0xFFu, s >> 24));
     const uint32_t g16 = (smax - 6u) & 0xFFFFu;
-    const uint32_t s_i = (s >> (8 * ((uint32_t)(i & 15) >> 2))) & 0xFFu;
-    const uint32_t offset = (((g16 - s_i) & 0xFFFFu) << 7) & 0xFFFFu;
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t byte = (c[u] >> (8 * k)) & 0xFFu;
-      const uint32_t a0 = (e2m1_to_bf16_bits(byte & 0xFu) - offset) & 0xFFFFu;
-      const uint32_t a1 = (e2m1_to_bf16_bits(byte >> 4) - offset) & 0xFFFFu;
-      const float f0 = fmaxf(-448.0f, fminf(448.0f, bf16_to_f32(a0)));
-      const float f1 = fmaxf(-448.0f, fminf(448.0f, bf16_to_f32(a1)));
-      const uint32_t pr = fp8x2_from_f32(f0, f1);
-      if (k < 2) lo |= pr << (16 * k); else hi |= pr << (16 * (k - 2));
+    const uint32_t s_i = (s >> (8 * ((uint32_t)(i & 7) >> 1))) & 0xFFu;
+    const uint32_t adj = (g16 - s_i) & 0xFFFFu;
+    const int d = (int)(adj & 511u) - ((adj & 256u) ? 512 : 0);
+    u32x2 o0, o1;
+    if ((unsigned)(d + 6) <= 11u) {
+      o0 = to_fp8_dword_fast(c[u][0], d);
+      o1 = to_fp8_dword_fast(c[u][1], d);
+    } else {
+      const uint32_t offset = (adj << 7) & 0xFFFFu;
+      o0 = to_fp8_dword_ref(c[u][0], offset);
+      o1 = to_fp8_dword_ref(c[u][1], offset);
     }
-    u32x2 o;
-    o[0] = lo;
-    o[1] = hi;
-    __builtin_nontemporal_store(o, out + i);
-    if ((i & 15) == 0) {
-      const uint32_t G = (uint32_t)(i >> 4);
+    u32x4 o;
+    o[0] = o0[0];
+    o[1] = o0[1];
+    o[2] = o1[0];
+    o[3] = o1[1];
+    out[i] = o;
+    if ((i & 7) == 0) {
+      const uint32_t G = (uint32_t)(i >> 3);
       const uint32_t row = G / gpr, col = G - row * gpr;
       out_s[(int64_t)col * M + row] = __uint_as_float((g16 & 0xFFu) << 23);
     }
@@ -76,13 +131,13 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint32_t* __res
 
 hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
                                hipStream_t stream) {
-  const int64_t ndw = M * Kb / 4;
-  if (ndw == 0) return hipSuccess;
+  const int64_t npairs = M * Kb / 8;
+  if (npairs == 0) return hipSuccess;
   constexpr int U = 4;
-  const int64_t blocks = (ndw + 256 * U - 1) / (256 * U);
+  const int64_t blocks = (npairs + 256 * U - 1) / (256 * U);
   hipLaunchKernelGGL((mxfp4_to_fp8_kernel<U>), dim3((unsigned)blocks), dim3(256), 0, stream,
-                     static_cast<const uint32_t*>(q), static_cast<const uint32_t*>(s), static_cast<u32x2*>(out),
-                     out_s, ndw, (uint32_t)M, (uint32_t)(Kb / 64));
+                     static_cast<const u32x2*>(q), static_cast<const uint32_t*>(s), static_cast<u32x4*>(out), out_s,
+                     npairs, (uint32_t)M, (uint32_t)(Kb / 64));
   return hipGetLastError();
 }
 
