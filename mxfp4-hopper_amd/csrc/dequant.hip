@@ -37,20 +37,14 @@ __device__ __forceinline__ u32x4 dequant_dword_ref(uint32_t c, uint32_t sb) {
   return o;
 }
 
-// Fast path, valid for 1 <= sb <= 254. Each convert's result is pinned in a
-// VGPR: ROCm 7.2 otherwise mis-assigns the halves of the bf16x2 results.
-__device__ __forceinline__ uint32_t pin_u32(uint32_t w) {
-  asm volatile("" : "+v"(w));
-  return w;
-}
-
+// Fast path, valid for 1 <= sb <= 254.
 __device__ __forceinline__ u32x4 dequant_dword_fast(uint32_t c, uint32_t sb) {
   const float sc = __uint_as_float(sb << 23);
   u32x4 o;
-  o[0] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 0)));
-  o[1] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 1)));
-  o[2] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 2)));
-  o[3] = pin_u32(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, sc, 3)));
+  o[0] = cvt_pk_bf16_fp4<0>(c, sc);
+  o[1] = cvt_pk_bf16_fp4<1>(c, sc);
+  o[2] = cvt_pk_bf16_fp4<2>(c, sc);
+  o[3] = cvt_pk_bf16_fp4<3>(c, sc);
   return o;
 }
 

@@ -238,7 +238,7 @@ int omo_hip_quant_mxfp4_dual(const void* input, int64_t rows, int64_t cols, void
   REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", fn);
   REQUIRE(rows % 32 == 0 && cols % 32 == 0, "%s: rows and cols must be multiples of 32 (got %lld x %lld)", fn,
           (long long)rows, (long long)cols);
-  REQUIRE(rows / 32 <= 65535, "%s: rows/32 exceeds the grid limit", fn);
+  REQUIRE((rows / 32 + 1) * (cols / 256 + 1) < ((int64_t)1 << 30), "%s: too many tiles", fn);
   REQUIRE(std::isfinite(eps), "%s: eps must be finite", fn);
   const int64_t n = rows * cols;
   REQUIRE_BUF("input", input, n, n);

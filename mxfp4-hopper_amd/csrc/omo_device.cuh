@@ -17,13 +17,36 @@ typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// A dword of two bf16 as the vector operand of the gfx950 scaled converts.
-// The empty asm pins the value in a VGPR: without it, ROCm 7.2's compiler
-// feeds element 0 of a u32x4 to every __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16
-// that reads elements 1..3 (it emits a single dword load for all four).
-__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t w) {
-  asm volatile("" : "+v"(w));
-  return __builtin_bit_cast(bf16x2_t, w);
+// gfx950 scaled FP4 converts, written as (non-volatile) inline asm.
+// ROCm 7.2's lowering of __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16 feeds
+// element 0 of a u32x4 to the converts that name elements 1..3, and the
+// bf16x2 results of __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4 get their
+// halves mis-assigned; the asm form is opaque to that lowering and still
+// schedules freely. op_sel selects the byte of the 32-bit destination
+// (pk_fp4_bf16) or of the source (pk_bf16_fp4).
+//
+// cvt_pk_fp4<B>(old, src, scale): byte B of `old` = the two E2M1 nibbles of
+// the bf16 pair `src` (element 0 in the low nibble) divided by `scale`,
+// round-to-nearest-even, saturating at +-6.
+template <int B>
+__device__ __forceinline__ uint32_t cvt_pk_fp4(uint32_t old, uint32_t src, float scale) {
+  if constexpr (B == 0) asm("v_cvt_scalef32_pk_fp4_bf16 %0, %1, %2" : "+v"(old) : "v"(src), "v"(scale));
+  else if constexpr (B == 1) asm("v_cvt_scalef32_pk_fp4_bf16 %0, %1, %2 op_sel:[0,0,1,0]" : "+v"(old) : "v"(src), "v"(scale));
+  else if constexpr (B == 2) asm("v_cvt_scalef32_pk_fp4_bf16 %0, %1, %2 op_sel:[0,0,0,1]" : "+v"(old) : "v"(src), "v"(scale));
+  else asm("v_cvt_scalef32_pk_fp4_bf16 %0, %1, %2 op_sel:[0,0,1,1]" : "+v"(old) : "v"(src), "v"(scale));
+  return old;
+}
+
+// cvt_pk_bf16_fp4<B>(src, scale): the two E2M1 nibbles of byte B of `src`
+// times `scale`, as a bf16 pair (low nibble in the low half).
+template <int B>
+__device__ __forceinline__ uint32_t cvt_pk_bf16_fp4(uint32_t src, float scale) {
+  uint32_t r;
+  if constexpr (B == 0) asm("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2" : "=v"(r) : "v"(src), "v"(scale));
+  else if constexpr (B == 1) asm("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2 op_sel:[1,0,0]" : "=v"(r) : "v"(src), "v"(scale));
+  else if constexpr (B == 2) asm("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2 op_sel:[0,1,0]" : "=v"(r) : "v"(src), "v"(scale));
+  else asm("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2 op_sel:[1,1,0]" : "=v"(r) : "v"(src), "v"(scale));
+  return r;
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
@@ -86,6 +109,20 @@ __device__ __forceinline__ uint32_t e2m1_from_f32_ref(float q) {
   uint32_t r = (((e << 2) | m2) + inc) >> 1;
   r = r > 7u ? 7u : r;
   return ((sign >> 28) | r) & 0xFu;
+}
+
+// cvt_pk_f32_fp4<B>(src, scale, &lo, &hi): the two E2M1 nibbles of byte B
+// of `src` times `scale`, as two fp32 values (exact for scale 2^k).
+template <int B>
+__device__ __forceinline__ void cvt_pk_f32_fp4(uint32_t src, float scale, float* lo, float* hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  f32x2_t r;
+  if constexpr (B == 0) asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2" : "=v"(r) : "v"(src), "v"(scale));
+  else if constexpr (B == 1) asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[1,0,0]" : "=v"(r) : "v"(src), "v"(scale));
+  else if constexpr (B == 2) asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[0,1,0]" : "=v"(r) : "v"(src), "v"(scale));
+  else asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[1,1,0]" : "=v"(r) : "v"(src), "v"(scale));
+  *lo = r[0];
+  *hi = r[1];
 }
 
 // IEEE binary32 -> bf16 bits, round to nearest even; NaN -> 0x7FFF.

@@ -55,10 +55,10 @@ __device__ __forceinline__ uint32_t quant_chunk_fast(const u32x4& d, uint32_t am
   *byte = (uint32_t)(c + 127);
   float y_s = exp2i(c);
   uint32_t r = 0;
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[0]), y_s, 0);
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[1]), y_s, 1);
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[2]), y_s, 2);
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(d[3]), y_s, 3);
+  r = cvt_pk_fp4<0>(r, d[0], y_s);
+  r = cvt_pk_fp4<1>(r, d[1], y_s);
+  r = cvt_pk_fp4<2>(r, d[2], y_s);
+  r = cvt_pk_fp4<3>(r, d[3], y_s);
   return r;
 }
 
@@ -82,10 +82,10 @@ __device__ __forceinline__ u32x4 quant_block32_fast(const uint32_t (&p)[16], uin
 #pragma unroll
   for (int w = 0; w < 4; w++) {
     uint32_t r = 0;
-    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 0]), y_s, 0);
-    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 1]), y_s, 1);
-    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 2]), y_s, 2);
-    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, as_bf16x2(p[4 * w + 3]), y_s, 3);
+    r = cvt_pk_fp4<0>(r, p[4 * w + 0], y_s);
+    r = cvt_pk_fp4<1>(r, p[4 * w + 1], y_s);
+    r = cvt_pk_fp4<2>(r, p[4 * w + 2], y_s);
+    r = cvt_pk_fp4<3>(r, p[4 * w + 3], y_s);
     out[w] = r;
   }
   return out;

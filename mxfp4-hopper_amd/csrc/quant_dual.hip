@@ -4,43 +4,65 @@
 // The columnwise output is defined by the TE integration as
 // quant_rowwise(X.T.contiguous()) (code/transformer_engine-2.8.diff:1463-1466):
 // codes [K, M/2] and scales [K, M/32]. The reference pays a full transpose
-// copy plus a second quantize pass for it; here each 32x256 input tile is
-// read once, quantized rowwise from registers (same DPP-quad scheme as the
-// rowwise kernel) and staged in LDS, from where each thread reads one
-// 32-element column and quantizes it along M. Both layouts use the
+// copy plus a second quantize pass for it. Both layouts here use the
 // reference block rule (code/kernel/per_token_quant_mxfp4.cu:151-254) with
 // fp4_min = -6, fp4_max = 6, the constants of the quantize wrapper
 // (code/kernel/api/mxfp4.py:11-12, 152-154).
+//
+// Tiles are 64 rows x 256 columns (32 KiB of bf16). Each lane loads 8 chunks
+// of 16 B (two rows of 512 B per wave and load); the rowwise blocks are
+// quantized from registers exactly as in the rowwise kernel (a block is a
+// DPP quad) and their codes leave as full 128 B lines. The tile is staged in
+// LDS; each lane then reads one dword (two adjacent columns) from 32
+// consecutive rows, repacks the two columns into bf16 pairs with v_perm_b32
+// and quantizes both 32-element column blocks (16 B of codes each).
+//
+// Tile order is XCD-aware: workgroup b runs on XCD b % 8, so the tiles are
+// numbered so that each XCD takes a contiguous run of tiles that walks down
+// M first. The four vertically adjacent tiles that fill one 128 B line of
+// columnwise codes then run at the same time behind the same L2.
 #include "omo_internal.h"
 #include "omo_quant.cuh"
 
 namespace omo_hip {
 
-constexpr int kDualRows = 32;
+constexpr int kDualRows = 64;
 constexpr int kDualCols = 256;
 constexpr int kDualPitch = kDualCols * 2 + 16;  // bytes per LDS row
+constexpr int kXcds = 8;
 
 __global__ __launch_bounds__(256) void quant_dual_kernel(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
                                                          uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
-                                                         uint8_t* __restrict__ col_s, int64_t M, int64_t K, float eps,
-                                                         int c_eps) {
+                                                         uint8_t* __restrict__ col_s, int64_t M, int64_t K,
+                                                         int tiles_m, int tiles, int per_xcd, float eps, int c_eps) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
   const int t = threadIdx.x;
-  const int64_t k0 = (int64_t)blockIdx.x * kDualCols, m0 = (int64_t)blockIdx.y * kDualRows;
-  // 32 rows x 32 chunks of 8 bf16; thread t owns chunks t + 256 k.
-  u32x4 d[4];
+  const int b = blockIdx.x;
+  const int logical = (b % kXcds) * per_xcd + b / kXcds;
+  if (logical >= tiles) return;
+  const int64_t mt = logical % tiles_m, kt = logical / tiles_m;
+  const int64_t m0 = mt * kDualRows, k0 = kt * kDualCols;
+  const int rows_valid = (int)(M - m0 < kDualRows ? M - m0 : kDualRows);  // 32 or 64
+  // ---- load: 64 rows x 32 chunks of 8 bf16; lane owns chunks t + 256 k.
+  // Chunks outside the tensor load from a clamped in-bounds address (and are
+  // ignored below), so every load is unconditional.
+  u32x4 d[8];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < 8; k++) {
     const int cid = t + 256 * k, r = cid >> 5, cc = cid & 31;
     const int64_t col = k0 + cc * 8;
-    if (col < K) d[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (m0 + r) * K + col));
+    const int rr = r < rows_valid ? r : rows_valid - 1;
+    const int64_t cl = col < K ? col : K - 8;
+    d[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (m0 + rr) * K + cl));
   }
+  // ---- rowwise blocks from registers; stage the tile in LDS
   const bool quad_leader = (t & 3) == 0;
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < 8; k++) {
     const int cid = t + 256 * k, r = cid >> 5, cc = cid & 31;
     const int64_t col = k0 + cc * 8;
-    if (col >= K) continue;  // K % 32 == 0: a quad is entirely in or out
+    // K % 32 == 0 and rows_valid is uniform per row: a quad is entirely in or out
+    if (r >= rows_valid || col >= K) continue;
     *reinterpret_cast<u32x4*>(tile + r * kDualPitch + cc * 16) = d[k];
     uint32_t codes, byte;
     const uint32_t am = quad_max_u32(chunk_absmax_bits(d[k]));
@@ -50,39 +72,52 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint16_t* __restr
       quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
     }
     const int64_t grow = m0 + r;
-    __builtin_nontemporal_store(codes, row_q + (grow * K + col) / 8);
+    row_q[(grow * K + col) / 8] = codes;
     if (quad_leader) row_s[grow * (K / 32) + col / 32] = (uint8_t)byte;
   }
   __syncthreads();
-  const int64_t kc = k0 + t;
-  if (kc >= K) return;
-  uint32_t p[16];
-  uint32_t amax_bits = 0;
+  // ---- columnwise: lane owns columns 2p, 2p+1 of row block g (32 rows)
+  const int p = t & 127, g = t >> 7;
+  const int64_t kc = k0 + 2 * p;
+  if (32 * g >= rows_valid || kc >= K) return;
+  uint32_t ca[16], cb[16];
+  uint32_t amax_a = 0, amax_b = 0;
 #pragma unroll
   for (int j = 0; j < 16; j++) {
-    const uint32_t lo = *reinterpret_cast<const uint16_t*>(tile + (2 * j) * kDualPitch + 2 * t);
-    const uint32_t hi = *reinterpret_cast<const uint16_t*>(tile + (2 * j + 1) * kDualPitch + 2 * t);
-    p[j] = lo | (hi << 16);
-    amax_bits = max(amax_bits, max(lo & 0x7FFFu, hi & 0x7FFFu));
+    const uint32_t w0 = *reinterpret_cast<const uint32_t*>(tile + (32 * g + 2 * j) * kDualPitch + 4 * p);
+    const uint32_t w1 = *reinterpret_cast<const uint32_t*>(tile + (32 * g + 2 * j + 1) * kDualPitch + 4 * p);
+    ca[j] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);  // column 2p: rows 2j (low), 2j+1 (high)
+    cb[j] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);  // column 2p+1
+    amax_a = pk_max_u16(amax_a, ca[j] & 0x7FFF7FFFu);
+    amax_b = pk_max_u16(amax_b, cb[j] & 0x7FFF7FFFu);
   }
-  uint32_t byte;
-  u32x4 codes;
-  if (amax_bits < 0x7F80u) {
-    codes = quant_block32_fast(p, amax_bits, eps, c_eps, &byte);
-  } else {
-    codes = quant_block32_ref(p, eps, -6.0f, 6.0f, &byte);
-  }
-  __builtin_nontemporal_store(codes, reinterpret_cast<u32x4*>(col_q + kc * (M / 2) + m0 / 2));
-  col_s[kc * (M / 32) + m0 / 32] = (uint8_t)byte;
+  amax_a = max(amax_a & 0xFFFFu, amax_a >> 16);
+  amax_b = max(amax_b & 0xFFFFu, amax_b >> 16);
+  uint32_t byte_a, byte_b;
+  u32x4 qa, qb;
+  if (amax_a < 0x7F80u) qa = quant_block32_fast(ca, amax_a, eps, c_eps, &byte_a);
+  else qa = quant_block32_ref(ca, eps, -6.0f, 6.0f, &byte_a);
+  if (amax_b < 0x7F80u) qb = quant_block32_fast(cb, amax_b, eps, c_eps, &byte_b);
+  else qb = quant_block32_ref(cb, eps, -6.0f, 6.0f, &byte_b);
+  const int64_t mo = (m0 + 32 * g) / 2;
+  *reinterpret_cast<u32x4*>(col_q + kc * (M / 2) + mo) = qa;
+  *reinterpret_cast<u32x4*>(col_q + (kc + 1) * (M / 2) + mo) = qb;
+  const int64_t so = (m0 + 32 * g) / 32;
+  col_s[kc * (M / 32) + so] = (uint8_t)byte_a;
+  col_s[(kc + 1) * (M / 32) + so] = (uint8_t)byte_b;
 }
 
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
                              float eps, hipStream_t stream) {
   if (M == 0 || K == 0) return hipSuccess;
-  dim3 grid((unsigned)((K + kDualCols - 1) / kDualCols), (unsigned)(M / kDualRows));
-  hipLaunchKernelGGL(quant_dual_kernel, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
-                     static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s), static_cast<uint8_t*>(col_q),
-                     static_cast<uint8_t*>(col_s), M, K, eps, host_c_eps(eps, 6.0f));
+  const int64_t tiles_m = (M + kDualRows - 1) / kDualRows;
+  const int64_t tiles_k = (K + kDualCols - 1) / kDualCols;
+  const int64_t tiles = tiles_m * tiles_k;
+  const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
+  hipLaunchKernelGGL(quant_dual_kernel, dim3((unsigned)(per_xcd * kXcds)), dim3(256), 0, stream,
+                     static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
+                     static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, (int)tiles_m, (int)tiles,
+                     (int)per_xcd, eps, host_c_eps(eps, 6.0f));
   return hipGetLastError();
 }
 

@@ -18,152 +18,256 @@
 // out_s = 1/scale at [(soff_i + tile) * N + c], q = v * scale, and the
 // split's output block [N, len_i] starts at off_i * N.
 //
-// Both kernels stage the tile's code bytes (8 KiB) and scale bytes in LDS
-// and recompute v from them; each thread owns one output column segment of
-// 64 rows so the FP8 stores are 16 B vectors along M.
+// One 512-thread block per tile. The tile's code bytes (128 rows x 64 B) and
+// scale bytes are staged in LDS. Lane t owns code-byte column p = t/8 (two
+// element columns) and the 16 rows of eighth q = t%8, so 8 adjacent lanes
+// hold a full tile column: the column amax is two quad_perm steps and one
+// row_half_mirror step of DPP, and the eight lanes write the column's 128
+// output rows as eight contiguous 16 B pieces.
+// When all 16 scale bytes of a lane lie in [1, 252] no product can be inf
+// or NaN, and v_cvt_scalef32_pk_f32_fp4 gives both columns' exact fp32
+// values of a row in one instruction; otherwise the lane restates the
+// reference per element.
 #include "omo_device.cuh"
 #include "omo_internal.h"
 
 namespace omo_hip {
 
 constexpr int kTile = 128;
-constexpr int kCodePitch = 64 + 4;  // code bytes per tile row (+pad)
+constexpr int kCodePitch = 64 + 16;  // LDS bytes per code row (16 B aligned rows)
 
-struct TileSmem {
+constexpr int kRcThreads = 512;
+
+// LDS row of tile row r: the 8 lanes of a column read rows 16q + j at the
+// same time; storing row 16q + j at 8j + q puts those rows at consecutive LDS
+// rows (distinct banks) instead of 16 rows apart (the same bank).
+__device__ __forceinline__ int lds_row(int r) { return ((r & 15) << 3) | (r >> 4); }
+
+// Maximum over the 8 lanes 8k..8k+7 (all active).
+__device__ __forceinline__ float oct_fmax(float v) {
+  v = quad_fmax(v);
+  // row_half_mirror (0x141): lane i of each 8-lane half-row reads lane 7 - i
+  const float o = __uint_as_float((uint32_t)__builtin_amdgcn_mov_dpp((int)__float_as_uint(v), 0x141, 0xF, 0xF, false));
+  return fmaxf(v, o);
+}
+
+struct RowColSmem {
   uint8_t codes[kTile * kCodePitch];
-  uint8_t scales[kTile][4];
-  float part[2][kTile];
-  float mult[kTile];
+  uint8_t scales[4][kTile];  // [MX block of the tile][row]
 };
 
-// Stage the codes/scales of tile rows [row0, row0 + rows_valid) and element
-// columns [col0, col0 + 128) into LDS; out-of-range bytes become 0.
-__device__ __forceinline__ void stage_tile(TileSmem& sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
-                                           int64_t N, int64_t row0, int rows_valid, int64_t col0, bool vec_ok) {
+// A lane's share of one tile's staging data: one 16 B chunk of codes and,
+// for lanes 0..127, the four scale bytes of one row.
+struct StageRegs {
+  u32x4 codes;
+  uint32_t scales;
+};
+
+// Load the staging data of tile rows [row0, row0 + rows_valid), element
+// columns [col0, col0 + 128). Missing codes become 0; missing scales 127
+// (1.0), so out-of-tensor elements dequantize to exactly 0 on the fast path.
+__device__ __forceinline__ StageRegs rc_load(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, int64_t N,
+                                             int64_t row0, int rows_valid, int64_t col0, bool vin) {
   const int t = threadIdx.x;
   const int64_t half = N / 2, sstride = N / 32;
-#pragma unroll
-  for (int k = 0; k < 2; k++) {
-    const int cidx = t + 256 * k;  // 512 chunks of 16 code bytes
-    const int r = cidx >> 2, c16 = cidx & 3;
-    const int64_t gcol = col0 + c16 * 32;  // first element of the chunk
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
+  StageRegs g;
+  {
+    const int r = t >> 2, c16 = t & 3;  // 512 chunks of 16 code bytes, one per lane
+    const int64_t gcol = col0 + c16 * 32;
+    u32x4 w = {0u, 0u, 0u, 0u};
     if (r < rows_valid && gcol < N) {
       const uint8_t* src = q + (row0 + r) * half + gcol / 2;
-      if (vec_ok && gcol + 32 <= N) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(src);
-        w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+      if (vin && gcol + 32 <= N) {
+        w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
       } else {
         const int nb = (int)((N - gcol) / 2 < 16 ? (N - gcol) / 2 : 16);
         for (int j = 0; j < nb; j++) w[j >> 2] |= (uint32_t)src[j] << (8 * (j & 3));
       }
     }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(sm.codes + r * kCodePitch + c16 * 16);
-    dst[0] = w[0]; dst[1] = w[1]; dst[2] = w[2]; dst[3] = w[3];
+    g.codes = w;
   }
-  if (t < kTile) {
-    uint32_t sv = 0;
-    if (t < rows_valid) {
+  g.scales = 0x7F7F7F7Fu;
+  if (t < kTile && t < rows_valid) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int64_t gcol = col0 + 32 * j;
-        // the reference indexes scales with row stride N/32 (floor)
-        if (gcol < N) sv |= (uint32_t)s[(row0 + t) * sstride + gcol / 32] << (8 * j);
-      }
+    for (int j = 0; j < 4; j++) {
+      const int64_t gcol = col0 + 32 * j;
+      // the reference indexes scales with row stride N/32 (floor)
+      if (gcol < N) g.scales = (g.scales & ~(0xFFu << (8 * j))) | ((uint32_t)s[(row0 + t) * sstride + gcol / 32] << (8 * j));
     }
-    *reinterpret_cast<uint32_t*>(&sm.scales[t][0]) = sv;
+  }
+  return g;
+}
+
+__device__ __forceinline__ void rc_put(RowColSmem& sm, const StageRegs& g) {
+  const int t = threadIdx.x;
+  *reinterpret_cast<u32x4*>(sm.codes + lds_row(t >> 2) * kCodePitch + (t & 3) * 16) = g.codes;
+  if (t < kTile) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) sm.scales[j][t] = (uint8_t)(g.scales >> (8 * j));
   }
 }
 
-// Dequantized value of tile element (r, c), 0 outside the tensor.
-__device__ __forceinline__ float tile_value(const TileSmem& sm, int r, int c, bool valid) {
-  const uint32_t byte = sm.codes[r * kCodePitch + (c >> 1)];
-  const uint32_t nib = (c & 1) ? (byte >> 4) : (byte & 0xFu);
-  const float sc = bf16_to_f32((uint32_t)sm.scales[r][c >> 5] << 7);
-  const float v = bf16_to_f32(e2m1_to_bf16_bits(nib)) * sc;
-  return valid ? v : 0.0f;
+// Output of one lane: the fp8 bytes of its 16 rows for both element columns.
+struct LaneCols {
+  u32x4 e0, e1;
+};
+
+// scale bytes 1..252 in every byte of w (no zero byte, no byte >= 253)
+__device__ __forceinline__ bool bytes_in_1_252(uint32_t w) {
+  const uint32_t zero = (w - 0x01010101u) & ~w & 0x80808080u;
+  const uint32_t big = ((w & 0x7F7F7F7Fu) + 0x03030303u) & w & 0x80808080u;
+  return (zero | big) == 0u;
 }
 
-// amax over the tile column c (seeded with `seed`), combined over 2 halves.
-__device__ __forceinline__ float tile_column_amax(TileSmem& sm, int rows_valid, bool col_valid, float seed) {
-  const int t = threadIdx.x, c = t & (kTile - 1), h = t >> 7;
-  float m = seed;
-  for (int r = h * 64; r < h * 64 + 64; r++) m = fmaxf(m, fabsf(tile_value(sm, r, c, col_valid && r < rows_valid)));
-  sm.part[h][c] = m;
-  __syncthreads();
-  return fmaxf(sm.part[0][c], sm.part[1][c]);
-}
-
-// Quantize the tile column owned by this thread (rows h*64 .. h*64+63) with
-// multiplier `mult` and write it to dst[0 .. rows) (dst = column base).
-__device__ __forceinline__ void tile_column_store(const TileSmem& sm, int c, int h, int rows_valid, bool col_valid,
-                                                  float mult, uint8_t* __restrict__ dst, bool vec_ok) {
+template <bool MSPLIT>
+__device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t N, int64_t col0, float seed, float eps,
+                                        float* __restrict__ out_s_row, LaneCols& res) {
+  const int t = threadIdx.x, p = t >> 3, qq = t & 7;
+  const int blk = p >> 4;
+  const bool col_valid = col0 + 2 * p < N;  // N is even: both columns or neither
+  uint32_t sw[4], cb[16];
 #pragma unroll
-  for (int r16 = 0; r16 < 64; r16 += 16) {
-    const int rb = h * 64 + r16;
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
+  for (int j4 = 0; j4 < 4; j4++) sw[j4] = *reinterpret_cast<const uint32_t*>(&sm.scales[blk][16 * qq + 4 * j4]);
+#pragma unroll
+  for (int j = 0; j < 16; j++) cb[j] = sm.codes[lds_row(16 * qq + j) * kCodePitch + p];
+  const bool fast = bytes_in_1_252(sw[0]) && bytes_in_1_252(sw[1]) && bytes_in_1_252(sw[2]) && bytes_in_1_252(sw[3]);
+  auto scale_of = [&](int j) { return __uint_as_float(((sw[j >> 2] >> (8 * (j & 3))) & 0xFFu) << 23); };
+  float a0 = seed, a1 = seed;
+  if (fast) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      float v0, v1;
+      cvt_pk_f32_fp4<0>(cb[j], scale_of(j), &v0, &v1);
+      a0 = fmaxf(a0, fabsf(v0));
+      a1 = fmaxf(a1, fabsf(v1));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const bool ok = col_valid && (16 * qq + j) < rows_valid;
+      const float sc = bf16_to_f32(((sw[j >> 2] >> (8 * (j & 3))) & 0xFFu) << 7);
+      const float v0 = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j] & 0xFu)) * sc : 0.0f;
+      const float v1 = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j] >> 4)) * sc : 0.0f;
+      a0 = fmaxf(a0, fabsf(v0));
+      a1 = fmaxf(a1, fabsf(v1));
+    }
+  }
+  a0 = oct_fmax(a0);
+  a1 = oct_fmax(a1);
+  float m0, m1, inv0, inv1;
+  if (MSPLIT) {
+    // compute_te_pow2_scale with FP8_E4M3_MAX = 448: multiplier 1/2^k, stored 2^k
+    auto pow2 = [eps](float amax, float* mult, float* inv) {
+      if (amax <= eps) { *mult = 1.0f; *inv = 1.0f; return; }
+      const uint32_t b = __float_as_uint(amax / 448.0f);
+      uint32_t e = (b >> 23) & 0xFFu;
+      if (b & 0x7FFFFFu) e += 1u;
+      *inv = __uint_as_float(e << 23);  // 2^(e-127); 0 for e == 0, inf for e == 255
+      if (e == 0u) *mult = __builtin_inff();
+      else if (e >= 255u) *mult = 0.0f;
+      else if (e == 254u) *mult = __uint_as_float(0x00400000u);  // 2^-127, subnormal
+      else *mult = exp2i(127 - (int)e);
+    };
+    pow2(a0, &m0, &inv0);
+    pow2(a1, &m1, &inv1);
+  } else {
+    inv0 = a0 / 448.0f;
+    inv1 = a1 / 448.0f;
+    m0 = (a0 > 1e-9f) ? (448.0f / a0) : 0.0f;
+    m1 = (a1 > 1e-9f) ? (448.0f / a1) : 0.0f;
+  }
+  if (qq == 0 && col_valid) {
+    out_s_row[2 * p] = inv0;
+    out_s_row[2 * p + 1] = inv1;
+  }
+  uint32_t w0[4] = {0u, 0u, 0u, 0u}, w1[4] = {0u, 0u, 0u, 0u};
+  // the NaN-free clamp below needs finite multipliers as well
+  if (fast && m0 < __builtin_inff() && m1 < __builtin_inff()) {
 #pragma unroll
     for (int j = 0; j < 16; j += 2) {
-      const float v0 = tile_value(sm, rb + j, c, col_valid && rb + j < rows_valid) * mult;
-      const float v1 = tile_value(sm, rb + j + 1, c, col_valid && rb + j + 1 < rows_valid) * mult;
-      const float q0 = fminf(fmaxf(v0, -448.0f), 448.0f);
-      const float q1 = fminf(fmaxf(v1, -448.0f), 448.0f);
-      w[j >> 2] |= fp8x2_from_f32(q0, q1) << (8 * (j & 3));
+      float v00, v01, v10, v11;
+      cvt_pk_f32_fp4<0>(cb[j], scale_of(j), &v00, &v01);
+      cvt_pk_f32_fp4<0>(cb[j + 1], scale_of(j + 1), &v10, &v11);
+      // finite products and multipliers: a NaN-free clamp
+      const float x0 = __builtin_amdgcn_fmed3f(v00 * m0, -448.0f, 448.0f);
+      const float x1 = __builtin_amdgcn_fmed3f(v10 * m0, -448.0f, 448.0f);
+      const float y0 = __builtin_amdgcn_fmed3f(v01 * m1, -448.0f, 448.0f);
+      const float y1 = __builtin_amdgcn_fmed3f(v11 * m1, -448.0f, 448.0f);
+      w0[j >> 2] |= fp8x2_from_f32(x0, x1) << (8 * (j & 3));
+      w1[j >> 2] |= fp8x2_from_f32(y0, y1) << (8 * (j & 3));
     }
-    if (rb >= rows_valid) break;
-    if (vec_ok && rb + 16 <= rows_valid) {
-      u32x4 o;
-      o[0] = w[0]; o[1] = w[1]; o[2] = w[2]; o[3] = w[3];
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst + rb));
-    } else {
-      for (int j = 0; j < 16 && rb + j < rows_valid; j++) dst[rb + j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      float v[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const bool ok = col_valid && (16 * qq + j + h) < rows_valid;
+        const float sc = bf16_to_f32(((sw[(j + h) >> 2] >> (8 * ((j + h) & 3))) & 0xFFu) << 7);
+        v[h][0] = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j + h] & 0xFu)) * sc : 0.0f;
+        v[h][1] = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j + h] >> 4)) * sc : 0.0f;
+      }
+      const float x0 = fminf(fmaxf(v[0][0] * m0, -448.0f), 448.0f);
+      const float x1 = fminf(fmaxf(v[1][0] * m0, -448.0f), 448.0f);
+      const float y0 = fminf(fmaxf(v[0][1] * m1, -448.0f), 448.0f);
+      const float y1 = fminf(fmaxf(v[1][1] * m1, -448.0f), 448.0f);
+      w0[j >> 2] |= fp8x2_from_f32(x0, x1) << (8 * (j & 3));
+      w1[j >> 2] |= fp8x2_from_f32(y0, y1) << (8 * (j & 3));
+    }
+  }
+  res.e0 = u32x4{w0[0], w0[1], w0[2], w0[3]};
+  res.e1 = u32x4{w1[0], w1[1], w1[2], w1[3]};
+}
+
+// Write a lane's 16 bytes of one output column (rows 16q .. 16q+15 of the
+// tile) to dst[0 .. 16), stopping at rows_valid.
+__device__ __forceinline__ void rc_store(uint8_t* __restrict__ dst, const u32x4& w, int r_base, int rows_valid,
+                                         bool vec_ok) {
+  if (vec_ok && r_base + 16 <= rows_valid) {
+    *reinterpret_cast<u32x4*>(dst) = w;
+  } else {
+    for (int j = 0; j < 16 && r_base + j < rows_valid; j++) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+  }
+}
+
+// Persistent over tiles (tile = blockIdx.x + k * gridDim.x, tile_m fastest):
+// the next tile's codes and scales are loaded into registers while the
+// current tile is converted, so reads and writes overlap.
+__global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_kernel(const uint8_t* __restrict__ q,
+                                                                    const uint8_t* __restrict__ s,
+                                                                    uint8_t* __restrict__ out, float* __restrict__ out_s,
+                                                                    int64_t M, int64_t N, int tiles_m, int tiles,
+                                                                    float eps, bool vin, bool vout) {
+  __shared__ RowColSmem sm;
+  int tile = blockIdx.x;
+  if (tile >= tiles) return;
+  auto rows_of = [&](int tl) { const int64_t r0 = (int64_t)(tl % tiles_m) * kTile; return (int)(M - r0 < kTile ? M - r0 : kTile); };
+  StageRegs g = rc_load(q, s, N, (int64_t)(tile % tiles_m) * kTile, rows_of(tile), (int64_t)(tile / tiles_m) * kTile, vin);
+  const int t = threadIdx.x, p = t >> 3, qq = t & 7;
+  for (; tile < tiles; tile += gridDim.x) {
+    const int64_t bm = tile % tiles_m, bn = tile / tiles_m;
+    const int64_t row0 = bm * kTile, col0 = bn * kTile;
+    const int rows_valid = rows_of(tile);
+    __syncthreads();  // the previous tile's LDS reads are done
+    rc_put(sm, g);
+    __syncthreads();
+    const int nxt = tile + gridDim.x;
+    if (nxt < tiles) g = rc_load(q, s, N, (int64_t)(nxt % tiles_m) * kTile, rows_of(nxt), (int64_t)(nxt / tiles_m) * kTile, vin);
+    LaneCols res;
+    rc_tile<false>(sm, rows_valid, N, col0, eps, eps, out_s + bm * N + col0, res);
+    const int64_t c = col0 + 2 * p;
+    if (c < N) {
+      rc_store(out + c * M + row0 + 16 * qq, res.e0, 16 * qq, rows_valid, vout);
+      rc_store(out + (c + 1) * M + row0 + 16 * qq, res.e1, 16 * qq, rows_valid, vout);
     }
   }
 }
 
-__global__ __launch_bounds__(256) void row_to_fp8_col_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
-                                                             uint8_t* __restrict__ out, float* __restrict__ out_s,
-                                                             int64_t M, int64_t N, float eps, bool vin, bool vout) {
-  __shared__ TileSmem sm;
-  const int64_t bm = blockIdx.x, bn = blockIdx.y;
-  const int64_t row0 = bm * kTile, col0 = bn * kTile;
-  const int rows_valid = (int)(M - row0 < kTile ? M - row0 : kTile);
-  stage_tile(sm, q, s, N, row0, rows_valid, col0, vin);
-  __syncthreads();
-  const int t = threadIdx.x, c = t & (kTile - 1);
-  const bool col_valid = col0 + c < N;
-  const float amax = tile_column_amax(sm, rows_valid, col_valid, eps);
-  if (t < kTile && col_valid) {
-    out_s[bm * N + col0 + c] = amax / 448.0f;
-    sm.mult[c] = (amax > 1e-9f) ? (448.0f / amax) : 0.0f;
-  } else if (t < kTile) {
-    sm.mult[c] = 0.0f;
-  }
-  __syncthreads();
-  const int oc = t >> 1, oh = t & 1;
-  if (col0 + oc < N) tile_column_store(sm, oc, oh, rows_valid, true, sm.mult[oc], out + (col0 + oc) * M + row0, vout);
-}
-
-// compute_te_pow2_scale with FP8_E4M3_MAX = 448: the multiplier 1/2^k and the
-// stored 1/multiplier, both exact powers of two (or 0 / inf).
-__device__ __forceinline__ void te_pow2(float amax, float eps, float* mult, float* inv) {
-  if (amax <= eps) { *mult = 1.0f; *inv = 1.0f; return; }
-  const uint32_t b = __float_as_uint(amax / 448.0f);
-  uint32_t e = (b >> 23) & 0xFFu;
-  if (b & 0x7FFFFFu) e += 1u;
-  const float div = __uint_as_float(e << 23);  // 2^(e-127), 0 for e == 0, inf for e == 255
-  *inv = div;                                   // 1.0f / (1.0 / div) == div for these values
-  if (e == 0u) *mult = __builtin_inff();
-  else if (e >= 255u) *mult = 0.0f;
-  else if (e == 254u) *mult = __uint_as_float(0x00400000u);  // 2^-127, subnormal
-  else *mult = exp2i(127 - (int)e);
-}
-
-__global__ __launch_bounds__(256) void row_to_fp8_col_msplit_kernel(
+__global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
     int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin) {
-  __shared__ TileSmem sm;
+  __shared__ RowColSmem sm;
   const int64_t split = blockIdx.x, bm = blockIdx.y, bn = blockIdx.z;
   const int64_t len = lens[split];
   if (bm * kTile >= len) return;
@@ -173,24 +277,18 @@ __global__ __launch_bounds__(256) void row_to_fp8_col_msplit_kernel(
   if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
   const int64_t row0 = start + bm * kTile, col0 = bn * kTile;
   const int rows_valid = (int)(len - bm * kTile < kTile ? len - bm * kTile : kTile);
-  stage_tile(sm, q, s, N, row0, rows_valid, col0, vin);
+  rc_put(sm, rc_load(q, s, N, row0, rows_valid, col0, vin));
   __syncthreads();
-  const int t = threadIdx.x, c = t & (kTile - 1);
-  const bool col_valid = col0 + c < N;
-  const float amax = tile_column_amax(sm, rows_valid, col_valid, 0.0f);
-  if (t < kTile) {
-    float mult = 0.0f, inv = 0.0f;
-    te_pow2(amax, eps, &mult, &inv);
-    sm.mult[c] = mult;
-    if (col_valid) out_s[(sstart + bm) * N + col0 + c] = inv;
-  }
-  __syncthreads();
-  const int oc = t >> 1, oh = t & 1;
-  if (col0 + oc < N) {
-    uint8_t* dst = out + start * N + (col0 + oc) * len + bm * kTile;
-    const bool vout = ((start * N + (col0 + oc) * len + bm * kTile) & 15) == 0 &&
-                      ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
-    tile_column_store(sm, oc, oh, rows_valid, true, sm.mult[oc], dst, vout);
+  LaneCols res;
+  rc_tile<true>(sm, rows_valid, N, col0, 0.0f, eps, out_s + (sstart + bm) * N + col0, res);
+  const int t = threadIdx.x, p = t >> 3, qq = t & 7;
+  const int64_t c = col0 + 2 * p;
+  if (c < N) {
+    const int64_t o0 = start * N + c * len + bm * kTile + 16 * qq;
+    const int64_t o1 = o0 + len;
+    const bool base_al = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    rc_store(out + o0, res.e0, 16 * qq, rows_valid, base_al && (o0 & 15) == 0);
+    rc_store(out + o1, res.e1, 16 * qq, rows_valid, base_al && (o1 & 15) == 0);
   }
 }
 
@@ -199,9 +297,21 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
   if (M == 0 || N == 0) return hipSuccess;
   const bool vin = (N % 32 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
   const bool vout = (M % 16 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
-  dim3 grid((unsigned)((M + kTile - 1) / kTile), (unsigned)((N + kTile - 1) / kTile));
-  hipLaunchKernelGGL(row_to_fp8_col_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
-                     static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, M, N, eps, vin, vout);
+  const int64_t tiles_m = (M + kTile - 1) / kTile, tiles = tiles_m * ((N + kTile - 1) / kTile);
+  // one wave of resident blocks: two 512-thread blocks per CU at this
+  // kernel's register use (4 waves per SIMD)
+  static int grid_cap = 0;
+  if (grid_cap == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    grid_cap = 2 * cus;
+  }
+  const int64_t grid = tiles < grid_cap ? tiles : grid_cap;
+  hipLaunchKernelGGL(row_to_fp8_col_kernel, dim3((unsigned)grid), dim3(kRcThreads), 0, stream,
+                     static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
+                     M, N, (int)tiles_m, (int)tiles, eps, vin, vout);
   return hipGetLastError();
 }
 
@@ -213,7 +323,7 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   if (nsplits == 0 || max_split_len <= 0 || N == 0) return hipSuccess;
   const bool vin = (N % 32 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
   dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)((N + kTile - 1) / kTile));
-  hipLaunchKernelGGL(row_to_fp8_col_msplit_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
+  hipLaunchKernelGGL(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
                      out_s_rows, eps, vin);
   return hipGetLastError();

@@ -332,6 +332,37 @@ def test_row_to_fp8_col_wide_scales(oracle, dev):
     np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
+@pytest.mark.parametrize("lo,hi", [(1, 4), (250, 254), (1, 252), (0, 3)])
+def test_row_to_fp8_col_scale_edges(oracle, dev, lo, hi):
+    """Scale bytes at the ends of the range: subnormal products (1..4), the
+    last bytes before overflow (250..254), and byte 0 (value 0)."""
+    _say("row_to_fp8_col scale edges", lo, hi)
+    omo = _omo()
+    rng = np.random.default_rng(lo * 1000 + hi)
+    M, N = 384, 1024
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(lo, hi + 1, size=(M, N // 32)).astype(np.uint8)
+    for fn, outs_rows in (("dense", (M + 127) // 128), ("msplit", None)):
+        if fn == "dense":
+            out = torch.empty((N, M), dtype=FP8, device=dev)
+            outs = torch.empty((outs_rows, N), dtype=torch.float32, device=dev)
+            omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out,
+                                                     outs, 1e-10)
+            torch.cuda.synchronize()
+            eo, es = oracle.row_to_fp8_col(q, s)
+            np.testing.assert_array_equal(bits_u8(out), eo)
+            np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+        else:
+            from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper
+            splits = [100, 284]
+            ys, ss = omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper(torch.from_numpy(q).to(dev),
+                                                                         torch.from_numpy(s).to(dev), splits)
+            torch.cuda.synchronize()
+            eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+            np.testing.assert_array_equal(np.concatenate([bits_u8(y).reshape(-1) for y in ys]), eo)
+            np.testing.assert_array_equal(torch.cat(ss).cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
 # ------------------------------------------------------- row -> col (msplit)
 @pytest.mark.parametrize("splits,N", [([1, 127, 128, 300], 256), ([0, 5, 0, 2048, 129], 7168), ([128], 128),
                                       ([2000, 1800, 2300, 2100], 2048)])
