@@ -24,9 +24,7 @@
 namespace omo_hip {
 
 // ---------------------------------------------------------------- rowwise
-// Each lane converts one code dword (8 elements) into 8 FP8 bytes; 16 lanes
-// cover one group. A wave reads 256 contiguous code bytes and writes 512
-// contiguous FP8 bytes per instruction.
+// A code dword (8 elements) becomes 8 FP8 bytes; a lane converts two of them.
 //
 // The reference subtracts off = 128 * (adjust mod 512) from the bf16 pattern
 // of each code, adjust = (uint16)(g - s_i). Write d for the signed value of
@@ -76,30 +74,42 @@ __device__ __forceinline__ u32x2 to_fp8_dword_ref(uint32_t c, uint32_t offset) {
   return o;
 }
 
-// Each lane converts two code dwords (16 elements of one MX block, 8 B) into
-// 16 FP8 bytes, so loads and stores are contiguous across the wave (2 KiB
-// of codes read and 4 KiB of FP8 written per wave and step); 8 lanes cover
-// one 128-element group.
+// Block tile: kRqRows rows x kRqGroups groups of 128 elements (256 code
+// bytes per row, 8 KiB per block). Lane e of the tile (e = u * 256 + t)
+// converts code pair c = e % (8 kRqGroups) of tile row e / (8 kRqGroups):
+// 16 B stores, contiguous over 16-lane row pieces. The fp32 scales of a tile
+// land in kRqGroups runs of kRqRows consecutive floats of the transposed
+// scale tensor [K/128, M], each written whole by one block, so no 128 B line
+// of it is assembled from partial writes of several workgroups on different
+// XCDs. Codes are read and FP8 bytes written non-temporally (streamed once).
+constexpr int kRqGroups = 4;
+constexpr int kRqRows = 32;
 template <int UNROLL>
 __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restrict__ q,
                                                            const uint32_t* __restrict__ s4,
                                                            u32x4* __restrict__ out, float* __restrict__ out_s,
-                                                           int64_t npairs, uint32_t M, uint32_t gpr) {
-  const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
+                                                           uint32_t M, uint32_t gpr, uint32_t gx) {
+  constexpr int PPR = 8 * kRqGroups;  // pairs per tile row
+  const uint32_t bx = blockIdx.x % gx, by = blockIdx.x / gx;
+  const int64_t ppr_all = 8 * (int64_t)gpr;
   u32x2 c[UNROLL];
   uint32_t sd[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
-    const int64_t i = base + (int64_t)u * 256;
-    if (i < npairs) {
+    const int e = u * 256 + threadIdx.x;
+    const uint32_t r = by * kRqRows + e / PPR, cp = bx * PPR + e % PPR;
+    if (r < M && cp < 8 * gpr) {
+      const int64_t i = (int64_t)r * ppr_all + cp;
       c[u] = __builtin_nontemporal_load(q + i);
       sd[u] = s4[i >> 3];
     }
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
-    const int64_t i = base + (int64_t)u * 256;
-    if (i >= npairs) continue;
+    const int e = u * 256 + threadIdx.x;
+    const uint32_t r = by * kRqRows + e / PPR, cp = bx * PPR + e % PPR;
+    if (r >= M || cp >= 8 * gpr) continue;
+    const int64_t i = (int64_t)r * ppr_all + cp;
     const uint32_t s = sd[u];
     const uint32_t smax = max(max(s & 0xFFu, (s >> 8) & 0xFFu), max((s >> 16) & 0xFFu, s >> 24));
     const uint32_t g16 = (smax - 6u) & 0xFFFFu;
@@ -120,24 +130,20 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restri
     o[1] = o0[1];
     o[2] = o1[0];
     o[3] = o1[1];
-    out[i] = o;
-    if ((i & 7) == 0) {
-      const uint32_t G = (uint32_t)(i >> 3);
-      const uint32_t row = G / gpr, col = G - row * gpr;
-      out_s[(int64_t)col * M + row] = __uint_as_float((g16 & 0xFFu) << 23);
-    }
+    __builtin_nontemporal_store(o, out + i);
+    if ((cp & 7) == 0) out_s[(int64_t)(cp >> 3) * M + r] = __uint_as_float((g16 & 0xFFu) << 23);
   }
 }
 
 hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
                                hipStream_t stream) {
-  const int64_t npairs = M * Kb / 8;
-  if (npairs == 0) return hipSuccess;
-  constexpr int U = 4;
-  const int64_t blocks = (npairs + 256 * U - 1) / (256 * U);
-  hipLaunchKernelGGL((mxfp4_to_fp8_kernel<U>), dim3((unsigned)blocks), dim3(256), 0, stream,
+  if (M == 0 || Kb == 0) return hipSuccess;
+  constexpr int U = kRqRows * 8 * kRqGroups / 256;
+  const int64_t gpr = Kb / 64;
+  const int64_t gx = (gpr + kRqGroups - 1) / kRqGroups, gy = (M + kRqRows - 1) / kRqRows;
+  hipLaunchKernelGGL((mxfp4_to_fp8_kernel<U>), dim3((unsigned)(gx * gy)), dim3(256), 0, stream,
                      static_cast<const u32x2*>(q), static_cast<const uint32_t*>(s), static_cast<u32x4*>(out), out_s,
-                     npairs, (uint32_t)M, (uint32_t)(Kb / 64));
+                     (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
   return hipGetLastError();
 }
 

@@ -53,7 +53,8 @@ __device__ __forceinline__ float oct_fmax(float v) {
 
 struct RowColSmem {
   uint8_t codes[kTile * kCodePitch];
-  uint8_t scales[4][kTile];  // [MX block of the tile][row]
+  uint32_t fscales[4][kTile];  // s << 23: the fp32 pattern of 2^(s-127), [MX block of the tile][row]
+  uint8_t scales[4][kTile];    // the scale bytes themselves
 };
 
 // A lane's share of one tile's staging data: one 16 B chunk of codes and,
@@ -66,8 +67,11 @@ struct StageRegs {
 // Load the staging data of tile rows [row0, row0 + rows_valid), element
 // columns [col0, col0 + 128). Missing codes become 0; missing scales 127
 // (1.0), so out-of-tensor elements dequantize to exactly 0 on the fast path.
+// vin: 16 B vector code loads are allowed (N % 32 == 0, aligned base);
+// vs: a scale row's four bytes of the tile are one aligned dword
+// (N % 128 == 0, 4 B aligned base). The byte fallbacks keep exact bounds.
 __device__ __forceinline__ StageRegs rc_load(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, int64_t N,
-                                             int64_t row0, int rows_valid, int64_t col0, bool vin) {
+                                             int64_t row0, int rows_valid, int64_t col0, bool vin, bool vs) {
   const int t = threadIdx.x;
   const int64_t half = N / 2, sstride = N / 32;
   StageRegs g;
@@ -88,13 +92,32 @@ __device__ __forceinline__ StageRegs rc_load(const uint8_t* __restrict__ q, cons
   }
   g.scales = 0x7F7F7F7Fu;
   if (t < kTile && t < rows_valid) {
+    // the reference indexes scales with row stride N/32 (floor)
+    const uint8_t* srow = s + (row0 + t) * sstride + col0 / 32;
+    if (vs) {
+      g.scales = *reinterpret_cast<const uint32_t*>(srow);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int64_t gcol = col0 + 32 * j;
-      // the reference indexes scales with row stride N/32 (floor)
-      if (gcol < N) g.scales = (g.scales & ~(0xFFu << (8 * j))) | ((uint32_t)s[(row0 + t) * sstride + gcol / 32] << (8 * j));
+      for (int j = 0; j < 4; j++) {
+        if (col0 + 32 * j < N) g.scales = (g.scales & ~(0xFFu << (8 * j))) | ((uint32_t)srow[j] << (8 * j));
+      }
     }
   }
+  return g;
+}
+
+// Staging loads of an interior tile when every tile is whole and aligned
+// (M % 128 == 0, N % 128 == 0, 16 B aligned codes, 4 B aligned scales):
+// unconditional vector loads only, so the compiler can count the waits for
+// them separately from the stores still in flight. Lanes 128..511 load a
+// copy of the scale dword of row t % 128, which they do not use.
+__device__ __forceinline__ StageRegs rc_load_full(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                  int64_t N, int64_t row0, int64_t col0) {
+  const int t = threadIdx.x;
+  StageRegs g;
+  g.codes = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(q + (row0 + (t >> 2)) * (N / 2) + col0 / 2 + (t & 3) * 16));
+  g.scales = *reinterpret_cast<const uint32_t*>(s + (row0 + (t & (kTile - 1))) * (N / 32) + col0 / 32);
   return g;
 }
 
@@ -103,7 +126,11 @@ __device__ __forceinline__ void rc_put(RowColSmem& sm, const StageRegs& g) {
   *reinterpret_cast<u32x4*>(sm.codes + lds_row(t >> 2) * kCodePitch + (t & 3) * 16) = g.codes;
   if (t < kTile) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) sm.scales[j][t] = (uint8_t)(g.scales >> (8 * j));
+    for (int j = 0; j < 4; j++) {
+      const uint32_t b = (g.scales >> (8 * j)) & 0xFFu;
+      sm.scales[j][t] = (uint8_t)b;
+      sm.fscales[j][t] = b << 23;
+    }
   }
 }
 
@@ -119,6 +146,52 @@ __device__ __forceinline__ bool bytes_in_1_252(uint32_t w) {
   return (zero | big) == 0u;
 }
 
+// Value of lane `src` of the calling lane's wave.
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+}
+
+// Column scale factors from the column amax. Every lane of an 8-lane column
+// group holds a0, a1 (the amax of columns 2p, 2p+1); lanes q = 0..3 of the
+// group each compute one of the four results and the group reads them back,
+// so each lane runs one division instead of four.
+template <bool MSPLIT>
+__device__ __forceinline__ void rc_factors(float a0, float a1, float eps, float* m0, float* m1, float* inv0,
+                                           float* inv1) {
+  const int lane = (int)(threadIdx.x & 63), qq = lane & 7, base = lane & ~7;
+  const float a = (qq & 1) ? a1 : a0;
+  float mult, inv;
+  if (MSPLIT) {
+    // compute_te_pow2_scale with FP8_E4M3_MAX = 448: multiplier 1/2^k, stored 2^k
+    if (a <= eps) {
+      mult = 1.0f;
+      inv = 1.0f;
+    } else {
+      const uint32_t b = __float_as_uint(a / 448.0f);
+      uint32_t e = (b >> 23) & 0xFFu;
+      if (b & 0x7FFFFFu) e += 1u;
+      inv = __uint_as_float(e << 23);  // 2^(e-127); 0 for e == 0, inf for e == 255
+      if (e == 0u) mult = __builtin_inff();
+      else if (e >= 255u) mult = 0.0f;
+      else if (e == 254u) mult = __uint_as_float(0x00400000u);  // 2^-127, subnormal
+      else mult = exp2i(127 - (int)e);
+    }
+    *m0 = lane_value(mult, base);
+    *m1 = lane_value(mult, base + 1);
+    *inv0 = lane_value(inv, base);
+    *inv1 = lane_value(inv, base + 1);
+  } else {
+    // lanes q&2 == 0: 448 / amax (0 when amax <= 1e-9); q&2 != 0: amax / 448
+    const bool is_inv = (qq & 2) != 0;
+    float r = (is_inv ? a : 448.0f) / (is_inv ? 448.0f : a);
+    if (!is_inv && !(a > 1e-9f)) r = 0.0f;
+    *m0 = lane_value(r, base);
+    *m1 = lane_value(r, base + 1);
+    *inv0 = lane_value(r, base + 2);
+    *inv1 = lane_value(r, base + 3);
+  }
+}
+
 template <bool MSPLIT>
 __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t N, int64_t col0, float seed, float eps,
                                         float* __restrict__ out_s_row, LaneCols& res) {
@@ -126,18 +199,23 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
   const int blk = p >> 4;
   const bool col_valid = col0 + 2 * p < N;  // N is even: both columns or neither
   uint32_t sw[4], cb[16];
+  float sc[16];
 #pragma unroll
-  for (int j4 = 0; j4 < 4; j4++) sw[j4] = *reinterpret_cast<const uint32_t*>(&sm.scales[blk][16 * qq + 4 * j4]);
+  for (int j4 = 0; j4 < 4; j4++) {
+    sw[j4] = *reinterpret_cast<const uint32_t*>(&sm.scales[blk][16 * qq + 4 * j4]);
+    const u32x4 f = *reinterpret_cast<const u32x4*>(&sm.fscales[blk][16 * qq + 4 * j4]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) sc[4 * j4 + k] = __uint_as_float(f[k]);
+  }
 #pragma unroll
   for (int j = 0; j < 16; j++) cb[j] = sm.codes[lds_row(16 * qq + j) * kCodePitch + p];
   const bool fast = bytes_in_1_252(sw[0]) && bytes_in_1_252(sw[1]) && bytes_in_1_252(sw[2]) && bytes_in_1_252(sw[3]);
-  auto scale_of = [&](int j) { return __uint_as_float(((sw[j >> 2] >> (8 * (j & 3))) & 0xFFu) << 23); };
   float a0 = seed, a1 = seed;
   if (fast) {
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       float v0, v1;
-      cvt_pk_f32_fp4<0>(cb[j], scale_of(j), &v0, &v1);
+      cvt_pk_f32_fp4<0>(cb[j], sc[j], &v0, &v1);
       a0 = fmaxf(a0, fabsf(v0));
       a1 = fmaxf(a1, fabsf(v1));
     }
@@ -145,9 +223,9 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       const bool ok = col_valid && (16 * qq + j) < rows_valid;
-      const float sc = bf16_to_f32(((sw[j >> 2] >> (8 * (j & 3))) & 0xFFu) << 7);
-      const float v0 = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j] & 0xFu)) * sc : 0.0f;
-      const float v1 = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j] >> 4)) * sc : 0.0f;
+      const float s16 = bf16_to_f32(((sw[j >> 2] >> (8 * (j & 3))) & 0xFFu) << 7);
+      const float v0 = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j] & 0xFu)) * s16 : 0.0f;
+      const float v1 = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j] >> 4)) * s16 : 0.0f;
       a0 = fmaxf(a0, fabsf(v0));
       a1 = fmaxf(a1, fabsf(v1));
     }
@@ -155,46 +233,35 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
   a0 = oct_fmax(a0);
   a1 = oct_fmax(a1);
   float m0, m1, inv0, inv1;
-  if (MSPLIT) {
-    // compute_te_pow2_scale with FP8_E4M3_MAX = 448: multiplier 1/2^k, stored 2^k
-    auto pow2 = [eps](float amax, float* mult, float* inv) {
-      if (amax <= eps) { *mult = 1.0f; *inv = 1.0f; return; }
-      const uint32_t b = __float_as_uint(amax / 448.0f);
-      uint32_t e = (b >> 23) & 0xFFu;
-      if (b & 0x7FFFFFu) e += 1u;
-      *inv = __uint_as_float(e << 23);  // 2^(e-127); 0 for e == 0, inf for e == 255
-      if (e == 0u) *mult = __builtin_inff();
-      else if (e >= 255u) *mult = 0.0f;
-      else if (e == 254u) *mult = __uint_as_float(0x00400000u);  // 2^-127, subnormal
-      else *mult = exp2i(127 - (int)e);
-    };
-    pow2(a0, &m0, &inv0);
-    pow2(a1, &m1, &inv1);
-  } else {
-    inv0 = a0 / 448.0f;
-    inv1 = a1 / 448.0f;
-    m0 = (a0 > 1e-9f) ? (448.0f / a0) : 0.0f;
-    m1 = (a1 > 1e-9f) ? (448.0f / a1) : 0.0f;
-  }
+  rc_factors<MSPLIT>(a0, a1, eps, &m0, &m1, &inv0, &inv1);
   if (qq == 0 && col_valid) {
     out_s_row[2 * p] = inv0;
     out_s_row[2 * p + 1] = inv1;
   }
   uint32_t w0[4] = {0u, 0u, 0u, 0u}, w1[4] = {0u, 0u, 0u, 0u};
-  // the NaN-free clamp below needs finite multipliers as well
-  if (fast && m0 < __builtin_inff() && m1 < __builtin_inff()) {
+  // Dense: |v| <= amax and m = fl(448 / amax) bound |v * m| by 448 (1 + 2^-23),
+  // which E4M3 RNE rounds to 448 (only |x| > 464 overflows), so the clamp of
+  // the reference changes no byte. Grouped: the multiplier is a power of two
+  // that can exceed 448 / amax when amax <= eps, so the clamp stays; it needs
+  // finite multipliers to be NaN-free.
+  if (fast && (!MSPLIT || (m0 < __builtin_inff() && m1 < __builtin_inff()))) {
 #pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      float v00, v01, v10, v11;
-      cvt_pk_f32_fp4<0>(cb[j], scale_of(j), &v00, &v01);
-      cvt_pk_f32_fp4<0>(cb[j + 1], scale_of(j + 1), &v10, &v11);
-      // finite products and multipliers: a NaN-free clamp
-      const float x0 = __builtin_amdgcn_fmed3f(v00 * m0, -448.0f, 448.0f);
-      const float x1 = __builtin_amdgcn_fmed3f(v10 * m0, -448.0f, 448.0f);
-      const float y0 = __builtin_amdgcn_fmed3f(v01 * m1, -448.0f, 448.0f);
-      const float y1 = __builtin_amdgcn_fmed3f(v11 * m1, -448.0f, 448.0f);
-      w0[j >> 2] |= fp8x2_from_f32(x0, x1) << (8 * (j & 3));
-      w1[j >> 2] |= fp8x2_from_f32(y0, y1) << (8 * (j & 3));
+    for (int j4 = 0; j4 < 4; j4++) {
+      float x[4], y[4];  // rows 4 j4 + k of columns 2p (x), 2p + 1 (y)
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float v0, v1;
+        cvt_pk_f32_fp4<0>(cb[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
+        x[k] = v0 * m0;
+        y[k] = v1 * m1;
+        if (MSPLIT) {
+          x[k] = __builtin_amdgcn_fmed3f(x[k], -448.0f, 448.0f);
+          y[k] = __builtin_amdgcn_fmed3f(y[k], -448.0f, 448.0f);
+        }
+      }
+      // bytes 0, 1 from the low-word convert, bytes 2, 3 from the high-word one
+      w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
+      w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
     }
   } else {
 #pragma unroll
@@ -203,9 +270,9 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
 #pragma unroll
       for (int h = 0; h < 2; h++) {
         const bool ok = col_valid && (16 * qq + j + h) < rows_valid;
-        const float sc = bf16_to_f32(((sw[(j + h) >> 2] >> (8 * ((j + h) & 3))) & 0xFFu) << 7);
-        v[h][0] = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j + h] & 0xFu)) * sc : 0.0f;
-        v[h][1] = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j + h] >> 4)) * sc : 0.0f;
+        const float s16 = bf16_to_f32(((sw[(j + h) >> 2] >> (8 * ((j + h) & 3))) & 0xFFu) << 7);
+        v[h][0] = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j + h] & 0xFu)) * s16 : 0.0f;
+        v[h][1] = ok ? bf16_to_f32(e2m1_to_bf16_bits(cb[j + h] >> 4)) * s16 : 0.0f;
       }
       const float x0 = fminf(fmaxf(v[0][0] * m0, -448.0f), 448.0f);
       const float x1 = fminf(fmaxf(v[1][0] * m0, -448.0f), 448.0f);
@@ -232,41 +299,61 @@ __device__ __forceinline__ void rc_store(uint8_t* __restrict__ dst, const u32x4&
 
 // Persistent over tiles (tile = blockIdx.x + k * gridDim.x, tile_m fastest):
 // the next tile's codes and scales are loaded into registers while the
-// current tile is converted, so reads and writes overlap.
+// current tile is converted, so reads and writes overlap. FULL: every tile
+// is whole and aligned, and all loads and stores are unconditional vector
+// operations.
+template <bool FULL>
 __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_kernel(const uint8_t* __restrict__ q,
                                                                     const uint8_t* __restrict__ s,
                                                                     uint8_t* __restrict__ out, float* __restrict__ out_s,
                                                                     int64_t M, int64_t N, int tiles_m, int tiles,
-                                                                    float eps, bool vin, bool vout) {
+                                                                    float eps, bool vin, bool vs, bool vout) {
   __shared__ RowColSmem sm;
   int tile = blockIdx.x;
   if (tile >= tiles) return;
-  auto rows_of = [&](int tl) { const int64_t r0 = (int64_t)(tl % tiles_m) * kTile; return (int)(M - r0 < kTile ? M - r0 : kTile); };
-  StageRegs g = rc_load(q, s, N, (int64_t)(tile % tiles_m) * kTile, rows_of(tile), (int64_t)(tile / tiles_m) * kTile, vin);
+  auto rows_of = [&](int tl) {
+    if (FULL) return kTile;
+    const int64_t r0 = (int64_t)(tl % tiles_m) * kTile;
+    return (int)(M - r0 < kTile ? M - r0 : kTile);
+  };
+  auto load = [&](int tl) {
+    const int64_t r0 = (int64_t)(tl % tiles_m) * kTile, c0 = (int64_t)(tl / tiles_m) * kTile;
+    return FULL ? rc_load_full(q, s, N, r0, c0) : rc_load(q, s, N, r0, rows_of(tl), c0, vin, vs);
+  };
   const int t = threadIdx.x, p = t >> 3, qq = t & 7;
-  for (; tile < tiles; tile += gridDim.x) {
+  rc_put(sm, load(tile));
+  __syncthreads();
+  for (;;) {
     const int64_t bm = tile % tiles_m, bn = tile / tiles_m;
     const int64_t row0 = bm * kTile, col0 = bn * kTile;
     const int rows_valid = rows_of(tile);
-    __syncthreads();  // the previous tile's LDS reads are done
-    rc_put(sm, g);
-    __syncthreads();
-    const int nxt = tile + gridDim.x;
-    if (nxt < tiles) g = rc_load(q, s, N, (int64_t)(nxt % tiles_m) * kTile, rows_of(nxt), (int64_t)(nxt / tiles_m) * kTile, vin);
+    // Load the next tile (the last iteration reloads its own tile, unused)
+    // before this tile's stores: the wait for the load before the LDS put
+    // below then leaves this tile's stores in flight.
+    const int nxt = tile + (int)gridDim.x;
+    const StageRegs g = load(nxt < tiles ? nxt : tile);
     LaneCols res;
     rc_tile<false>(sm, rows_valid, N, col0, eps, eps, out_s + bm * N + col0, res);
     const int64_t c = col0 + 2 * p;
-    if (c < N) {
+    if (FULL) {
+      __builtin_nontemporal_store(res.e0, reinterpret_cast<u32x4*>(out + c * M + row0 + 16 * qq));
+      __builtin_nontemporal_store(res.e1, reinterpret_cast<u32x4*>(out + (c + 1) * M + row0 + 16 * qq));
+    } else if (c < N) {
       rc_store(out + c * M + row0 + 16 * qq, res.e0, 16 * qq, rows_valid, vout);
       rc_store(out + (c + 1) * M + row0 + 16 * qq, res.e1, 16 * qq, rows_valid, vout);
     }
+    if (nxt >= tiles) break;
+    tile = nxt;
+    __syncthreads();  // this tile's LDS reads are done
+    rc_put(sm, g);
+    __syncthreads();
   }
 }
 
 __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
-    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin) {
+    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs) {
   __shared__ RowColSmem sm;
   const int64_t split = blockIdx.x, bm = blockIdx.y, bn = blockIdx.z;
   const int64_t len = lens[split];
@@ -277,7 +364,7 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
   if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
   const int64_t row0 = start + bm * kTile, col0 = bn * kTile;
   const int rows_valid = (int)(len - bm * kTile < kTile ? len - bm * kTile : kTile);
-  rc_put(sm, rc_load(q, s, N, row0, rows_valid, col0, vin));
+  rc_put(sm, rc_load(q, s, N, row0, rows_valid, col0, vin, vs));
   __syncthreads();
   LaneCols res;
   rc_tile<true>(sm, rows_valid, N, col0, 0.0f, eps, out_s + (sstart + bm) * N + col0, res);
@@ -296,7 +383,9 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
                                  hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
   const bool vin = (N % 32 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
+  const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
   const bool vout = (M % 16 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
+  const bool full = vin && vs && vout && (M % kTile == 0);
   const int64_t tiles_m = (M + kTile - 1) / kTile, tiles = tiles_m * ((N + kTile - 1) / kTile);
   // one wave of resident blocks: two 512-thread blocks per CU at this
   // kernel's register use (4 waves per SIMD)
@@ -309,9 +398,10 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
     grid_cap = 2 * cus;
   }
   const int64_t grid = tiles < grid_cap ? tiles : grid_cap;
-  hipLaunchKernelGGL(row_to_fp8_col_kernel, dim3((unsigned)grid), dim3(kRcThreads), 0, stream,
-                     static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
-                     M, N, (int)tiles_m, (int)tiles, eps, vin, vout);
+  auto kernel = full ? row_to_fp8_col_kernel<true> : row_to_fp8_col_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
+                     static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, M, N, (int)tiles_m, (int)tiles,
+                     eps, vin, vs, vout);
   return hipGetLastError();
 }
 
@@ -322,10 +412,11 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   (void)out_capacity;  // the ABI layer checks out_capacity >= total_rows * N
   if (nsplits == 0 || max_split_len <= 0 || N == 0) return hipSuccess;
   const bool vin = (N % 32 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
+  const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
   dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)((N + kTile - 1) / kTile));
   hipLaunchKernelGGL(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
-                     out_s_rows, eps, vin);
+                     out_s_rows, eps, vin, vs);
   return hipGetLastError();
 }
 
