@@ -246,7 +246,21 @@ def main():
         out["payload_dequant_bf16"] = {"workload": "MXFP4->BF16 4096x7168",
                                        "kernel_GB/s": round(db / (t / steps * 1e-3) / 1e9, 1),
                                        "us_per_launch": round(t / steps * 1e3, 2)}
-        del q4, s4, f8, f8s, y4, x4
+        # transposed FP8 requant (fp8 [2W, M] + fp32 [M/128, 2W]) of the same payload
+        fc = [torch.empty((K, Mp), dtype=torch.float8_e4m3fn, device=dev) for _ in range(ps)]
+        fcs = [torch.empty((Mp // 128, K), dtype=torch.float32, device=dev) for _ in range(ps)]
+
+        def requant_col(i):
+            rc = lib.omo_hip_per_token_Mxfp4ToFp8_col(q4[i].data_ptr(), Mp, K // 2, s4[i].data_ptr(), n4 // 32,
+                                                      fc[i].data_ptr(), n4, fcs[i].data_ptr(), n4 // 128, 128,
+                                                      1e-10, -6.0, 6.0, 0, cur())
+            if rc:
+                _abi.check(rc)
+        t, _ = time_launches(torch, requant_col, ps, steps, 20)
+        out["payload_requant_fp8_col"] = {"workload": "MXFP4->FP8 E4M3 transposed 128x128 tiles 4096x7168",
+                                          "kernel_GB/s": round(rb / (t / steps * 1e-3) / 1e9, 1),
+                                          "us_per_launch": round(t / steps * 1e3, 2)}
+        del q4, s4, f8, f8s, y4, x4, fc, fcs
 
     if want("dual"):
         Mw, Kw = 7168, 18432

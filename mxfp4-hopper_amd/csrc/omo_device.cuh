@@ -141,6 +141,15 @@ __device__ __forceinline__ uint32_t fp8x2_from_f32(float a, float b) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
 }
 
+// Workgroup b of a 1-D grid is dispatched to XCD b % 8, and each XCD has its
+// own L2. This renumbers the grid so that XCD x takes one contiguous run of
+// logical indices (a bijection on [0, n)); workgroups adjacent in logical
+// order then share an L2, e.g. tiles that read the same scale lines.
+__device__ __forceinline__ uint32_t xcd_contiguous(uint32_t b, uint32_t n) {
+  const uint32_t x = b & 7u, j = b >> 3, q = n >> 3, r = n & 7u;
+  return x * q + (x < r ? x : r) + j;
+}
+
 // Exact ceil(log2(z)) for a finite normal float z > 0.
 __device__ __forceinline__ int ceil_log2_normal(float z) {
   uint32_t b = __float_as_uint(z);

@@ -90,7 +90,8 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restri
                                                            u32x4* __restrict__ out, float* __restrict__ out_s,
                                                            uint32_t M, uint32_t gpr, uint32_t gx) {
   constexpr int PPR = 8 * kRqGroups;  // pairs per tile row
-  const uint32_t bx = blockIdx.x % gx, by = blockIdx.x / gx;
+  const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x);
+  const uint32_t bx = L % gx, by = L / gx;
   const int64_t ppr_all = 8 * (int64_t)gpr;
   u32x2 c[UNROLL];
   uint32_t sd[UNROLL];
@@ -148,85 +149,125 @@ hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* o
 }
 
 // ------------------------------------------------------------ transposed
-// One 256-thread block per 128-row x 128-byte tile. The code tile and its
-// 128x8 scale bytes are staged in LDS; each thread then produces one output
-// row segment (one element column of the tile, 128 contiguous FP8 bytes =
-// a full 128 B line).
+// One 256-thread block per 128-row x 128-byte tile (256 element columns).
+//
+// The per-element rule of the reference (:244-290) is
+//   byte = E4M3(clamp(bf16((bits(code) - (adj << 7)) mod 2^16 & 0x7FFF)))
+// with adj = (uint8)(g - s_row). Subtracting a multiple of 128 never touches
+// the low 7 bits, and for a negative code the subtraction and the final
+// & 0x7FFF give the same pattern as for its magnitude (the sign bit only
+// changes where the borrow lands above bit 14, which the mask removes). So
+// the byte is a function of (adj, |code|) alone: a 256 x 8 table, built per
+// block in LDS by restating the reference rule for every entry. Each lane
+// then needs one 8-byte table row per tile row and v_perm_b32 lookups.
+//
+// Lane mapping (as in the row -> column FP8 kernel): lane t owns code-byte
+// column p (element columns 2p, 2p+1) and rows 16q .. 16q+15, q = t % 8; the
+// 8 lanes of a column write its 128 output rows as one full 128 B line per
+// store instruction. Four passes cover the tile's 128 byte columns.
 constexpr int kColTile = 128;
-constexpr int kColPitch = kColTile + 4;
+constexpr int kColPitch = kColTile + 16;  // 16 B aligned LDS rows
+
+struct ColSmem {
+  uint8_t codes[kColTile * kColPitch];
+  uint8_t scales[8][kColTile];   // [MX column of the tile][row]
+  uint32_t table[256][2];        // fp8 byte of |code| = 0..7 under adj (bytes 0..7)
+  uint32_t gpart[8][4];          // per MX column, per wave partial maxima
+};
+
+// LDS row of tile row r: rows 16q + j (q = 0..7) are read together, so they
+// are stored in consecutive LDS rows (distinct banks for pitch 144).
+__device__ __forceinline__ int col_lds_row(int r) { return ((r & 15) << 3) | (r >> 4); }
+
+// fp8 bytes of magnitudes 0..7 under adj, by the reference rule.
+__device__ __forceinline__ void col_table_row(uint32_t adj, uint32_t* lo, uint32_t* hi) {
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    const uint32_t a = ((e2m1_to_bf16_bits((uint32_t)c) - (adj << 7)) & 0xFFFFu) & 0x7FFFu;
+    const float f = fminf(fmaxf(bf16_to_f32(a), -448.0f), 448.0f);
+    w[c >> 2] |= (fp8x2_from_f32(f, f) & 0xFFu) << (8 * (c & 3));
+  }
+  *lo = w[0];
+  *hi = w[1];
+}
 
 __global__ __launch_bounds__(256) void mxfp4_to_fp8_col_kernel(const uint8_t* __restrict__ q,
                                                                const uint8_t* __restrict__ s,
                                                                uint8_t* __restrict__ out, float* __restrict__ out_s,
                                                                int64_t M, int64_t Kb, uint32_t eps8) {
-  __shared__ uint8_t tile[kColTile * kColPitch];
-  __shared__ uint8_t stile[kColTile][8];
-  __shared__ uint32_t gpart[4][8];
-  __shared__ uint32_t gcol[8];
+  __shared__ ColSmem sm;
   const int t = threadIdx.x;
-  const int64_t bx = blockIdx.x, by = blockIdx.y;
+  const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)(Kb / kColTile);
+  const int64_t bx = L % gx, by = L / gx;
   const int64_t row0 = by * kColTile;
-  const int64_t sstride = Kb / 16;
-  // codes: 128 rows x 128 B = 1024 chunks of 16 B
+  // ---- stage codes (1024 chunks of 16 B: 8 rows x 128 B per wave load) and scales
+  u32x4 cv[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const int cidx = t + 256 * k;
-    const int r = cidx >> 3, c16 = cidx & 7;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(q + (row0 + r) * Kb + bx * kColTile + c16 * 16);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(tile + r * kColPitch + c16 * 16);
-    dst[0] = v[0];
-    dst[1] = v[1];
-    dst[2] = v[2];
-    dst[3] = v[3];
+    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
+    cv[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + (row0 + r) * Kb + bx * kColTile + c16 * 16));
+  }
+  u32x2 sv = {0u, 0u};
+  if (t < kColTile) sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * (Kb / 16) + bx * 8);
+  {
+    uint32_t lo, hi;
+    col_table_row((uint32_t)t, &lo, &hi);
+    sm.table[t][0] = lo;
+    sm.table[t][1] = hi;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
+    *reinterpret_cast<u32x4*>(sm.codes + col_lds_row(r) * kColPitch + c16 * 16) = cv[k];
   }
   if (t < kColTile) {
-    const u32x2 sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * sstride + bx * 8);
-    *reinterpret_cast<u32x2*>(&stile[t][0]) = sv;
+#pragma unroll
+    for (int c = 0; c < 8; c++) sm.scales[c][t] = (uint8_t)(sv[c >> 2] >> (8 * (c & 3)));
   }
   __syncthreads();
-  // per MX column: max over 128 rows (seeded with (uint8)eps)
+  // ---- g per MX column: (uint8)(max(eps8, max over 128 rows) - 6)
   {
-    const int c = t & 7, rq = t >> 3;  // rows 4rq..4rq+3
-    uint32_t m = eps8;
+    const int c = t >> 5, r4 = (t & 31) * 4;  // a wave covers two MX columns
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(&sm.scales[c][r4]);
+    uint32_t m = max(max(w & 0xFFu, (w >> 8) & 0xFFu), max((w >> 16) & 0xFFu, w >> 24));
 #pragma unroll
-    for (int j = 0; j < 4; j++) m = max(m, (uint32_t)stile[rq * 4 + j][c]);
-    m = max(m, (uint32_t)__shfl_xor((int)m, 8));
-    m = max(m, (uint32_t)__shfl_xor((int)m, 16));
-    m = max(m, (uint32_t)__shfl_xor((int)m, 32));
-    if ((t & 63) < 8) gpart[t >> 6][c] = m;
+    for (int x = 1; x < 32; x <<= 1) m = max(m, (uint32_t)__shfl_xor((int)m, x));
+    if ((t & 31) == 0) sm.gpart[c][0] = (max(m, eps8) - 6u) & 0xFFu;
   }
   __syncthreads();
-  if (t < 8) {
-    const uint32_t m = max(max(gpart[0][t], gpart[1][t]), max(gpart[2][t], gpart[3][t]));
-    gcol[t] = (m - 6u) & 0xFFu;
-  }
-  __syncthreads();
-  // scale row by: 256 floats, entry j holds column j/32
-  out_s[by * (Kb * 2) + bx * 256 + t] = __uint_as_float(gcol[t >> 5] << 23);
-  // outputs: thread t -> element column e = t of the tile (byte t/2, nibble t&1)
-  const int b = t >> 1, h = t & 1, cblk = b >> 4;
-  const uint32_t g = gcol[cblk];
-  uint8_t* orow = out + (bx * 256 + t) * M + row0;
+  // scale row of the tile: 256 floats, entry e holds MX column e / 32 (:210-212)
+  __builtin_nontemporal_store(__uint_as_float(sm.gpart[t >> 5][0] << 23), out_s + by * (Kb * 2) + bx * 256 + t);
+  const int qq = t & 7;
+#pragma unroll 1
+  for (int pass = 0; pass < 4; pass++) {
+    const int p = 32 * pass + (t >> 3), cblk = p >> 4;
+    const uint32_t g = sm.gpart[cblk][0];
+    uint32_t r[16];
 #pragma unroll
-  for (int m16 = 0; m16 < kColTile; m16 += 16) {
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    for (int j4 = 0; j4 < 4; j4++) {
+      const uint32_t sw = *reinterpret_cast<const uint32_t*>(&sm.scales[cblk][16 * qq + 4 * j4]);
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-      const int r = m16 + j;
-      const uint32_t val = tile[r * kColPitch + b];
-      const uint32_t nib = h ? (val >> 4) : (val & 0xFu);
-      const uint32_t adj = (g - (uint32_t)stile[r][cblk]) & 0xFFu;
-      const uint32_t a = ((e2m1_to_bf16_bits(nib) - (adj << 7)) & 0xFFFFu) & 0x7FFFu;
-      const float f = fminf(fmaxf(bf16_to_f32(a), -448.0f), 448.0f);
-      const uint32_t byte = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f, f, 0, false) & 0xFFu;
-      w[j >> 2] |= byte << (8 * (j & 3));
+      for (int k = 0; k < 4; k++) {
+        const int j = 4 * j4 + k;
+        const uint32_t adj = (g - ((sw >> (8 * k)) & 0xFFu)) & 0xFFu;
+        const uint32_t cb = sm.codes[col_lds_row(16 * qq + j) * kColPitch + p];
+        const u32x2 tr = *reinterpret_cast<const u32x2*>(&sm.table[adj][0]);
+        // byte 0: element column 2p (low nibble), byte 1: 2p + 1 (high nibble)
+        const uint32_t sel = (cb & 0x7u) | ((cb << 4) & 0x700u) | 0x0C0C0000u;
+        r[j] = __builtin_amdgcn_perm(tr[1], tr[0], sel);
+      }
     }
-    u32x4 o;
-    o[0] = w[0];
-    o[1] = w[1];
-    o[2] = w[2];
-    o[3] = w[3];
-    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(orow + m16));
+    u32x4 oa, ob;
+#pragma unroll
+    for (int j4 = 0; j4 < 4; j4++) {
+      const uint32_t* rr = r + 4 * j4;
+      oa[j4] = __builtin_amdgcn_perm(rr[1], rr[0], 0x0C0C0400u) | (__builtin_amdgcn_perm(rr[3], rr[2], 0x0C0C0400u) << 16);
+      ob[j4] = __builtin_amdgcn_perm(rr[1], rr[0], 0x0C0C0501u) | (__builtin_amdgcn_perm(rr[3], rr[2], 0x0C0C0501u) << 16);
+    }
+    uint8_t* o = out + (bx * 256 + 2 * p) * M + row0 + 16 * qq;
+    __builtin_nontemporal_store(oa, reinterpret_cast<u32x4*>(o));
+    __builtin_nontemporal_store(ob, reinterpret_cast<u32x4*>(o + M));
   }
 }
 
@@ -235,7 +276,8 @@ hipError_t launch_mxfp4_to_fp8_col(const void* q, const void* s, void* out, floa
   if (M == 0 || Kb == 0) return hipSuccess;
   uint32_t eps8 = 0;
   if (eps > 0.0f) eps8 = eps >= 255.0f ? 255u : (uint32_t)eps;  // (uint8_t)eps, truncating
-  dim3 grid((unsigned)(Kb / kColTile), (unsigned)(M / kColTile));
+  // 1-D grid, tile index bx fastest, renumbered per XCD in the kernel
+  const dim3 grid((unsigned)((Kb / kColTile) * (M / kColTile)));
   hipLaunchKernelGGL(mxfp4_to_fp8_col_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, M, Kb, eps8);
   return hipGetLastError();

@@ -293,6 +293,39 @@ def test_to_fp8_col(oracle, dev, M, Kb, seed, spread, eps):
     np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
+def test_to_fp8_col_every_adjust(oracle, dev):
+    """Every (uint8)(g - s_row) value 0..255 meets every code byte. Row 0 of
+    each 128-row tile holds scale 255 (so g = 249 with eps = 1e-10); row r > 0
+    of tile k, MX column c holds 249 - a with a = (127 k + r - 1 + 37 c) mod 256,
+    so the adjust values of tiles 0..3 run through all 256 values. The code
+    bytes of a row run through all 256 values over two rows. The test asserts
+    the coverage before comparing with the oracle."""
+    _say("to_fp8_col every adjust value")
+    omo = _omo()
+    M, Kb = 512, 128
+    r = np.arange(M)
+    q = ((r[:, None] * 128 + np.arange(Kb)[None, :]) & 0xFF).astype(np.uint8)
+    k, rr = r // 128, r % 128
+    c = np.arange(Kb // 16)
+    a = (127 * k[:, None] + rr[:, None] - 1 + 37 * c[None, :]) % 256
+    s = np.where(rr[:, None] == 0, 255, (249 - a) % 256).astype(np.uint8)
+    adj_seen = set()
+    for k in range(M // 128):
+        blk = s[128 * k:128 * (k + 1)].astype(np.int64)
+        g = (blk.max(axis=0) - 6) & 0xFF
+        for cc in range(Kb // 16):
+            adj_seen.update(((g[cc] - blk[:, cc]) & 0xFF).tolist())
+    assert adj_seen == set(range(256))
+    qt, st = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
+    out = torch.empty((2 * Kb, M), dtype=FP8, device=dev)
+    outs = torch.empty((M // 128, 2 * Kb), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4ToFp8_col(qt, st, out, outs, 128, 1e-10, -6.0, 6.0, False)
+    torch.cuda.synchronize()
+    eo, es = oracle.mxfp4_to_fp8_col(q, s)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
 # ------------------------------------------------------- row -> col (dense)
 def payload_from_normal(M, K, seed, std=1.0):
     import oracle as o
