@@ -12,10 +12,11 @@
 // Tiles are 64 rows x 256 columns (32 KiB of bf16). Each lane loads 8 chunks
 // of 16 B (two rows of 512 B per wave and load); the rowwise blocks are
 // quantized from registers exactly as in the rowwise kernel (a block is a
-// DPP quad) and their codes leave as full 128 B lines. The tile is staged in
-// LDS; each lane then reads one dword (two adjacent columns) from 32
-// consecutive rows, repacks the two columns into bf16 pairs with v_perm_b32
-// and quantizes both 32-element column blocks (16 B of codes each).
+// DPP quad) and their codes leave as full 128 B lines (non-temporal
+// stores). The tile is staged in LDS; each lane then reads one dword (two
+// adjacent columns) from 32 consecutive rows, repacks the two columns into
+// bf16 pairs with v_perm_b32 and quantizes both 32-element column blocks
+// (16 B of codes each).
 //
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, so the tiles are
 // numbered so that each XCD takes a contiguous run of tiles that walks down
@@ -56,14 +57,19 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint16_t* __restr
     d[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (m0 + rr) * K + cl));
   }
   // ---- rowwise blocks from registers; stage the tile in LDS
+  // Lane t holds rows r0 + 8k (k = 0..7) of one 16 B column chunk cc, so its
+  // code, scale and LDS addresses advance by a fixed stride per k.
   const bool quad_leader = (t & 3) == 0;
+  const int r0 = t >> 5, cc = t & 31;
+  const int64_t col = k0 + cc * 8;
+  uint32_t* rq = row_q + (m0 + r0) * (K / 8) + col / 8;
+  uint8_t* rs = row_s + (m0 + r0) * (K / 32) + col / 32;
+  uint8_t* lt = tile + r0 * kDualPitch + cc * 16;
 #pragma unroll
   for (int k = 0; k < 8; k++) {
-    const int cid = t + 256 * k, r = cid >> 5, cc = cid & 31;
-    const int64_t col = k0 + cc * 8;
     // K % 32 == 0 and rows_valid is uniform per row: a quad is entirely in or out
-    if (r >= rows_valid || col >= K) continue;
-    *reinterpret_cast<u32x4*>(tile + r * kDualPitch + cc * 16) = d[k];
+    if (r0 + 8 * k >= rows_valid || col >= K) continue;
+    *reinterpret_cast<u32x4*>(lt + 8 * k * kDualPitch) = d[k];
     uint32_t codes, byte;
     const uint32_t am = quad_max_u32(chunk_absmax_bits(d[k]));
     if (am < 0x7F80u) {
@@ -71,9 +77,8 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint16_t* __restr
     } else {
       quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
     }
-    const int64_t grow = m0 + r;
-    row_q[(grow * K + col) / 8] = codes;
-    if (quad_leader) row_s[grow * (K / 32) + col / 32] = (uint8_t)byte;
+    __builtin_nontemporal_store(codes, rq + k * K);  // 8 rows down; streamed out
+    if (quad_leader) rs[k * (K / 4)] = (uint8_t)byte;
   }
   __syncthreads();
   // ---- columnwise: lane owns columns 2p, 2p+1 of row block g (32 rows)
