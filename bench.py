@@ -9,9 +9,10 @@ resident in HBM before the timed region. Four input/output buffer sets
 set. The script prints one JSON line.
 
 Also measured (extra keys): MXFP4 -> BF16 dequant of the same shape, the
-MoE-payload requant/dequant (4096 x 7168), the dual-layout quantize
-(7168 x 18432) and the row -> col FP8 conversion, each as GB/s of
-algorithmic bytes.
+MoE-payload requant/dequant (4096 x 7168, both FP8 layouts), the fused
+expert-parallel payload rows against Megatron's cat/split composition, the
+dual-layout quantize (7168 x 18432) and the row -> col FP8 conversion, each as
+GB/s of algorithmic bytes or microseconds per call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        [--only quant|dequant|...] [--copy-calibration]
@@ -37,7 +38,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (>= 3 to exceed the 256 MB cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of legs: quant,dequant,payload,dual,rowcol")
+    ap.add_argument("--only", default="", help="comma list of legs: quant,dequant,payload,ep_payload,dual,rowcol")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (known traffic) for counter calibration")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -261,6 +262,40 @@ def main():
                                           "kernel_GB/s": round(rb / (t / steps * 1e-3) / 1e9, 1),
                                           "us_per_launch": round(t / steps * 1e3, 2)}
         del q4, s4, f8, f8s, y4, x4, fc, fcs
+
+    if want("ep_payload"):
+        # expert-parallel payload rows [codes | scales] at cfg4's share (4096 x 7168): the fused
+        # kernels against Megatron's composition (quantize + torch.cat; two .contiguous() split
+        # copies + requant / dequant), all enqueued eagerly (torch's cat/copies allocate).
+        from omo_python_api import ep_payload as ep
+        from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
+        from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToFp8_wrapper
+        Tp, Hp = 4096, K
+        n5 = Tp * Hp
+        es = sets_for(wl.quant_bytes(n5) + wl.requant_fp8_bytes(n5), args.sets)
+        xe = [wl.normal_bf16((Tp, Hp), seed=60 + i, device=dev) for i in range(es)]
+        pe = [ep.fp4_quantize_packed(x) for x in xe]
+        steps = max(100, args.steps // 4)
+        res = {}
+        for name, fn in [
+            ("send_fused", lambda i: ep.fp4_quantize_packed(xe[i])),
+            ("send_unfused", lambda i: ep.pack_rowwise_components(*omo_per_token_group_quant_mxfp4(xe[i]))),
+            ("recv_fp8_fused", lambda i: ep.packed_mxfp4ToFp8(pe[i])),
+            ("recv_fp8_unfused", lambda i: omo_per_token_mxfp4ToFp8_wrapper(*ep.unpack_rowwise_components(pe[i]),
+                                                                             [Tp])),
+            ("recv_bf16_fused", lambda i: ep.packed_mxfp4ToBf16(pe[i])),
+        ]:
+            t, _ = time_launches(torch, fn, es, steps, 10, graph=False)
+            res[name] = round(t / steps * 1e3, 2)
+        out["ep_payload"] = {
+            "workload": "expert-parallel payload rows [T, 17H/32], T=4096, H=7168 (eager launches, us per call)",
+            "us": res,
+            "send_speedup": round(res["send_unfused"] / res["send_fused"], 3),
+            "recv_fp8_speedup": round(res["recv_fp8_unfused"] / res["recv_fp8_fused"], 3),
+            "send_fused_GB/s": round(wl.quant_bytes(n5) / (res["send_fused"] * 1e-6) / 1e9, 1),
+            "recv_fp8_fused_GB/s": round(wl.requant_fp8_bytes(n5) / (res["recv_fp8_fused"] * 1e-6) / 1e9, 1),
+        }
+        del xe, pe
 
     if want("dual"):
         Mw, Kw = 7168, 18432

@@ -137,6 +137,37 @@ OMO_API int omo_hip_quant_mxfp4_dual(const void* input, int64_t rows, int64_t co
                              void* row_s, int64_t row_s_bytes, void* col_q, int64_t col_q_bytes, void* col_s,
                              int64_t col_s_bytes, float eps, void* stream);
 
+/* Expert-parallel payload rows (code/megatron-0.15.0rc7.diff:32-63): row t
+ * of a [rows, 17*cols/32] uint8 tensor holds the row's MXFP4 codes (cols/2
+ * bytes) followed by its E8M0 scales (cols/32 bytes), the layout Megatron
+ * builds with torch.cat before the DeepEP dispatch and splits again with two
+ * .contiguous() copies after it. The three functions below write or read
+ * that layout in place. cols % 128 == 0 (dword-aligned rows).
+ *
+ * Quantize straight into payload rows. Replaces MXFP4Quantizer's quantize
+ * (omo_per_token_group_quant_fp4, code/kernel/ops.cu:28-29) followed by
+ * _pack_rowwise_components (code/megatron-0.15.0rc7.diff:93-99, called at
+ * :163-170). input [rows, cols] bf16 (16-byte aligned); output
+ * rows*17*cols/32 bytes (4-byte aligned); fp4 range fixed to +-6. */
+OMO_API int omo_hip_quant_mxfp4_packed(const void* input, int64_t rows, int64_t cols, void* output,
+                                       int64_t output_bytes, float eps, void* stream);
+
+/* MXFP4 -> BF16 dequant of payload rows into [rows, cols] bf16 (16-byte
+ * aligned). Replaces _unpack_rowwise_components (code/megatron-0.15.0rc7.diff:101-122)
+ * followed by omo_per_token_Mxfp4ToBf16_dequant (code/kernel/ops.cu:30-31).
+ * input 4-byte aligned. */
+OMO_API int omo_hip_packed_Mxfp4ToBf16_dequant(const void* input, int64_t rows, int64_t cols, void* output,
+                                               int64_t output_elems, void* stream);
+
+/* MXFP4 -> FP8 E4M3 rowwise requant of payload rows: output_q [rows, cols]
+ * fp8 (16-byte aligned) and output_s [cols/128, rows] fp32, the outputs of
+ * omo_per_token_Mxfp4ToFp8 (code/kernel/per_token_Mxfp4ToFp8.cu:86-309) on the
+ * unpacked tensors. Replaces _unpack_rowwise_components
+ * (code/megatron-0.15.0rc7.diff:101-122) followed by that requant. input
+ * 4-byte aligned. */
+OMO_API int omo_hip_packed_Mxfp4ToFp8(const void* input, int64_t rows, int64_t cols, void* output_q,
+                                      int64_t output_q_bytes, void* output_s, int64_t output_s_elems, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,51 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __res
   }
 }
 
+// Row-strided variant: row r's codes at q + r * q_stride, its scale bytes at
+// s + r * s_stride (bytes), output [rows, K] bf16 contiguous. Reads the
+// expert-parallel payload row [codes | scales] in place instead of the two
+// .contiguous() copies of its unpacking (code/megatron-0.15.0rc7.diff:101-122).
+// Workgroup b covers segment b % bpr of row b / bpr.
+template <int UNROLL>
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ q, int64_t q_stride,
+                                                           const uint8_t* __restrict__ s, int64_t s_stride,
+                                                           u32x4* __restrict__ out, int64_t K, int bpr) {
+  const int64_t row = blockIdx.x / (uint32_t)bpr;
+  const int seg = (int)(blockIdx.x - row * bpr);
+  const int dpr = (int)(K / 8);  // code dwords per row
+  const uint32_t* qr = reinterpret_cast<const uint32_t*>(q + row * q_stride);
+  const uint8_t* sr = s + row * s_stride;
+  u32x4* orow = out + row * dpr;
+  const int base = seg * (256 * UNROLL) + (int)threadIdx.x;
+  uint32_t c[UNROLL], sb[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const int i = base + u * 256;
+    if (i < dpr) {
+      c[u] = __builtin_nontemporal_load(qr + i);
+      sb[u] = sr[i >> 2];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const int i = base + u * 256;
+    if (i >= dpr) continue;
+    const u32x4 o = (sb[u] - 1u <= 253u) ? dequant_dword_fast(c[u], sb[u]) : dequant_dword_ref(c[u], sb[u]);
+    __builtin_nontemporal_store(o, orow + i);
+  }
+}
+
+hipError_t launch_dequant_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride, void* out,
+                               int64_t rows, int64_t K, hipStream_t stream) {
+  if (rows == 0 || K == 0) return hipSuccess;
+  constexpr int U = 4;
+  const int bpr = (int)((K / 8 + 256 * U - 1) / (256 * U));
+  hipLaunchKernelGGL((dequant_rows_kernel<U>), dim3((unsigned)(rows * bpr)), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(q), q_stride, static_cast<const uint8_t*>(s), s_stride,
+                     static_cast<u32x4*>(out), K, bpr);
+  return hipGetLastError();
+}
+
 hipError_t launch_dequant_bf16(const void* q, const void* s, void* out, int64_t nbytes, hipStream_t stream) {
   const int64_t ndw = nbytes / 4;
   if (ndw == 0) return hipSuccess;

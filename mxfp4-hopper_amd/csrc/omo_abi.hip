@@ -79,6 +79,14 @@ int requant_rowwise(const char* fn, const void* input, int64_t rows, int64_t row
                   fn);
 }
 
+// Payload rows [codes (cols/2 B) | scales (cols/32 B)], stride 17 cols / 32 bytes.
+int check_packed(const char* fn, int64_t rows, int64_t cols) {
+  REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", fn);
+  REQUIRE(cols % 128 == 0, "%s: cols must be a multiple of 128 (got %lld)", fn, (long long)cols);
+  REQUIRE(rows < ((int64_t)1 << 31) / (cols / 8 / 256 + 1), "%s: too many rows", fn);
+  return OMO_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -249,6 +257,59 @@ int omo_hip_quant_mxfp4_dual(const void* input, int64_t rows, int64_t cols, void
   REQUIRE(aligned(input, 16) && aligned(col_q, 16) && aligned(row_q, 4), "%s: misaligned buffer", fn);
   if (n == 0) return ok();
   return from_hip(omo_hip::launch_quant_dual(input, row_q, row_s, col_q, col_s, rows, cols, eps, as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_quant_mxfp4_packed(const void* input, int64_t rows, int64_t cols, void* output, int64_t output_bytes,
+                               float eps, void* stream) {
+  const char* fn = "omo_quant_mxfp4_packed";
+  int rc = check_packed(fn, rows, cols);
+  if (rc != OMO_OK) return rc;
+  REQUIRE(std::isfinite(eps), "%s: eps must be finite", fn);
+  const int64_t stride = cols / 32 * 17;
+  REQUIRE_BUF("input", input, rows * cols, rows * cols);
+  REQUIRE_BUF("output", output, output_bytes, rows * stride);
+  REQUIRE(aligned(input, 16) && aligned(output, 4), "%s: input must be 16-byte and output 4-byte aligned", fn);
+  if (rows == 0 || cols == 0) return ok();
+  uint8_t* out = static_cast<uint8_t*>(output);
+  return from_hip(omo_hip::launch_quant_rows(input, out, stride, out + cols / 2, stride, rows, cols, eps,
+                                             as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_packed_Mxfp4ToBf16_dequant(const void* input, int64_t rows, int64_t cols, void* output,
+                                       int64_t output_elems, void* stream) {
+  const char* fn = "omo_packed_Mxfp4ToBf16_dequant";
+  int rc = check_packed(fn, rows, cols);
+  if (rc != OMO_OK) return rc;
+  const int64_t stride = cols / 32 * 17;
+  REQUIRE_BUF("input", input, rows * stride, rows * stride);
+  REQUIRE_BUF("output", output, output_elems, rows * cols);
+  REQUIRE(aligned(input, 4) && aligned(output, 16), "%s: input must be 4-byte and output 16-byte aligned", fn);
+  if (rows == 0 || cols == 0) return ok();
+  const uint8_t* in = static_cast<const uint8_t*>(input);
+  return from_hip(omo_hip::launch_dequant_rows(in, stride, in + cols / 2, stride, output, rows, cols,
+                                               as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_packed_Mxfp4ToFp8(const void* input, int64_t rows, int64_t cols, void* output_q, int64_t output_q_bytes,
+                              void* output_s, int64_t output_s_elems, void* stream) {
+  const char* fn = "omo_packed_Mxfp4ToFp8";
+  int rc = check_packed(fn, rows, cols);
+  if (rc != OMO_OK) return rc;
+  REQUIRE(rows < ((int64_t)1 << 32) && cols / 128 * rows < ((int64_t)1 << 31), "%s: too many groups", fn);
+  const int64_t stride = cols / 32 * 17;
+  REQUIRE_BUF("input", input, rows * stride, rows * stride);
+  REQUIRE_BUF("output_q", output_q, output_q_bytes, rows * cols);
+  REQUIRE_BUF("output_s", output_s, output_s_elems, rows * (cols / 128));
+  REQUIRE(aligned(input, 4) && aligned(output_q, 16) && aligned(output_s, 4),
+          "%s: input needs 4-byte, output_q 16-byte, output_s 4-byte alignment", fn);
+  if (rows == 0 || cols == 0) return ok();
+  const uint8_t* in = static_cast<const uint8_t*>(input);
+  return from_hip(omo_hip::launch_mxfp4_to_fp8_rows(in, stride, in + cols / 2, stride, output_q,
+                                                    static_cast<float*>(output_s), rows, cols / 2,
+                                                    as_stream(stream)),
                   fn);
 }
 

@@ -27,6 +27,16 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
                                         int64_t nsplits, int64_t max_split_len, int64_t out_capacity,
                                         int64_t out_s_rows, float eps, hipStream_t stream);
 
+// Row-strided variants (bytes between consecutive rows of codes / scales).
+hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, int64_t s_stride, int64_t rows,
+                             int64_t K, float eps, hipStream_t stream);
+
+hipError_t launch_dequant_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride, void* out,
+                               int64_t rows, int64_t K, hipStream_t stream);
+
+hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride, void* out,
+                                    float* out_s, int64_t M, int64_t Kb, hipStream_t stream);
+
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
                              float eps, hipStream_t stream);
 

@@ -74,6 +74,73 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(QuantArgs a) {
   }
 }
 
+// Row-strided variant: row r of the codes starts at q + r * q_stride and its
+// scales at s + r * s_stride (bytes), so the outputs can be interleaved, e.g.
+// the expert-parallel payload row [codes (K/2 B) | scales (K/32 B)] that
+// Megatron builds with torch.cat (code/megatron-0.15.0rc7.diff:93-99,
+// 163-170). Workgroup b covers segment b % bpr of row b / bpr; a quad (one
+// block) never straddles rows because K % 32 == 0 and segments start at
+// multiples of 256 chunks. Reference rule with fp4_min = -6, fp4_max = 6.
+struct QuantRowsArgs {
+  const uint16_t* __restrict__ x;  // [rows, K] bf16
+  uint8_t* __restrict__ q;
+  uint8_t* __restrict__ s;
+  int64_t K, q_stride, s_stride;
+  int bpr;                         // workgroups per row
+  float eps;
+  int c_eps;
+};
+
+template <int UNROLL>
+__global__ __launch_bounds__(256) void quant_rows_kernel(QuantRowsArgs a) {
+  const int64_t row = blockIdx.x / (uint32_t)a.bpr;
+  const int seg = (int)(blockIdx.x - row * a.bpr);
+  const int cpr = (int)(a.K / 8);  // 16 B chunks per row
+  const u32x4* xr = reinterpret_cast<const u32x4*>(a.x + row * a.K);
+  uint32_t* qr = reinterpret_cast<uint32_t*>(a.q + row * a.q_stride);
+  uint8_t* sr = a.s + row * a.s_stride;
+  const int base = seg * (256 * UNROLL) + (int)threadIdx.x;
+  u32x4 d[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const int c = base + u * 256;
+    if (c < cpr) d[u] = __builtin_nontemporal_load(xr + c);
+  }
+  const bool quad_leader = (threadIdx.x & 3u) == 0u;
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const int c = base + u * 256;
+    if (c >= cpr) continue;  // whole quads
+    uint32_t codes, byte;
+    const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
+    if (am < 0x7F80u) {
+      codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
+    } else {
+      quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
+    }
+    __builtin_nontemporal_store(codes, qr + c);
+    if (quad_leader) sr[c >> 2] = (uint8_t)byte;
+  }
+}
+
+hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, int64_t s_stride, int64_t rows,
+                             int64_t K, float eps, hipStream_t stream) {
+  if (rows == 0 || K == 0) return hipSuccess;
+  constexpr int U = 2;
+  QuantRowsArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.q = static_cast<uint8_t*>(q);
+  a.s = static_cast<uint8_t*>(s);
+  a.K = K;
+  a.q_stride = q_stride;
+  a.s_stride = s_stride;
+  a.bpr = (int)((K / 8 + 256 * U - 1) / (256 * U));
+  a.eps = eps;
+  a.c_eps = host_c_eps(eps, 6.0f);
+  hipLaunchKernelGGL((quant_rows_kernel<U>), dim3((unsigned)(rows * a.bpr)), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, float eps, float fp4_min,
                                 float fp4_max, hipStream_t stream) {
   QuantArgs a;

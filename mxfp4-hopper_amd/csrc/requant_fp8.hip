@@ -84,9 +84,13 @@ __device__ __forceinline__ u32x2 to_fp8_dword_ref(uint32_t c, uint32_t offset) {
 // XCDs. Codes are read and FP8 bytes written non-temporally (streamed once).
 constexpr int kRqGroups = 4;
 constexpr int kRqRows = 32;
-template <int UNROLL>
-__global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restrict__ q,
-                                                           const uint32_t* __restrict__ s4,
+// Codes of row r start at q + r * q_stride and its scale bytes at
+// s + r * s_stride (bytes): contiguous [M, Kb] + [M, Kb/16] tensors, or the
+// expert-parallel payload rows [codes | scales] read in place. ALIGN8: the
+// code rows are 8-byte aligned (one 8 B load per lane, else two 4 B loads).
+template <int UNROLL, bool ALIGN8>
+__global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __restrict__ q, int64_t q_stride,
+                                                           const uint8_t* __restrict__ s, int64_t s_stride,
                                                            u32x4* __restrict__ out, float* __restrict__ out_s,
                                                            uint32_t M, uint32_t gpr, uint32_t gx) {
   constexpr int PPR = 8 * kRqGroups;  // pairs per tile row
@@ -100,9 +104,14 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restri
     const int e = u * 256 + threadIdx.x;
     const uint32_t r = by * kRqRows + e / PPR, cp = bx * PPR + e % PPR;
     if (r < M && cp < 8 * gpr) {
-      const int64_t i = (int64_t)r * ppr_all + cp;
-      c[u] = __builtin_nontemporal_load(q + i);
-      sd[u] = s4[i >> 3];
+      const uint8_t* src = q + r * q_stride + 8 * (int64_t)cp;
+      if (ALIGN8) {
+        c[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
+      } else {
+        c[u][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
+        c[u][1] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + 4));
+      }
+      sd[u] = *reinterpret_cast<const uint32_t*>(s + r * s_stride + 4 * (cp >> 3));
     }
   }
 #pragma unroll
@@ -111,10 +120,10 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restri
     const uint32_t r = by * kRqRows + e / PPR, cp = bx * PPR + e % PPR;
     if (r >= M || cp >= 8 * gpr) continue;
     const int64_t i = (int64_t)r * ppr_all + cp;
-    const uint32_t s = sd[u];
-    const uint32_t smax = max(max(s & 0xFFu, (s >> 8) & 0xFFu), max((s >> 16) & 0xFFu, s >> 24));
+    const uint32_t sw = sd[u];
+    const uint32_t smax = max(max(sw & 0xFFu, (sw >> 8) & 0xFFu), max((sw >> 16) & 0xFFu, sw >> 24));
     const uint32_t g16 = (smax - 6u) & 0xFFFFu;
-    const uint32_t s_i = (s >> (8 * ((uint32_t)(i & 7) >> 1))) & 0xFFu;
+    const uint32_t s_i = (sw >> (8 * ((cp & 7u) >> 1))) & 0xFFu;
     const uint32_t adj = (g16 - s_i) & 0xFFFFu;
     const int d = (int)(adj & 511u) - ((adj & 256u) ? 512 : 0);
     u32x2 o0, o1;
@@ -136,16 +145,23 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const u32x2* __restri
   }
 }
 
-hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
-                               hipStream_t stream) {
+hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride, void* out,
+                                    float* out_s, int64_t M, int64_t Kb, hipStream_t stream) {
   if (M == 0 || Kb == 0) return hipSuccess;
   constexpr int U = kRqRows * 8 * kRqGroups / 256;
   const int64_t gpr = Kb / 64;
   const int64_t gx = (gpr + kRqGroups - 1) / kRqGroups, gy = (M + kRqRows - 1) / kRqRows;
-  hipLaunchKernelGGL((mxfp4_to_fp8_kernel<U>), dim3((unsigned)(gx * gy)), dim3(256), 0, stream,
-                     static_cast<const u32x2*>(q), static_cast<const uint32_t*>(s), static_cast<u32x4*>(out), out_s,
-                     (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
+  const bool a8 = (q_stride % 8 == 0) && ((reinterpret_cast<uintptr_t>(q) & 7) == 0);
+  auto kernel = a8 ? mxfp4_to_fp8_kernel<U, true> : mxfp4_to_fp8_kernel<U, false>;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q), q_stride,
+                     static_cast<const uint8_t*>(s), s_stride, static_cast<u32x4*>(out), out_s, (uint32_t)M,
+                     (uint32_t)gpr, (uint32_t)gx);
   return hipGetLastError();
+}
+
+hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
+                               hipStream_t stream) {
+  return launch_mxfp4_to_fp8_rows(q, Kb, s, Kb / 16, out, out_s, M, Kb, stream);
 }
 
 // ------------------------------------------------------------ transposed

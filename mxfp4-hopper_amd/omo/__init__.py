@@ -37,6 +37,9 @@ __all__ = [
     "omo_per_token_Mxfp4ToFp8_col",
     "omo_per_token_Mxfp4ToFp8",
     "omo_quant_mxfp4_dual",
+    "omo_quant_mxfp4_packed",
+    "omo_packed_Mxfp4ToBf16_dequant",
+    "omo_packed_Mxfp4ToFp8",
 ]
 
 _FP8 = torch.float8_e4m3fn
@@ -257,3 +260,62 @@ def omo_quant_mxfp4_dual(input, row_q, row_s, col_q, col_s, eps=1e-10):
         _check(_lib.omo_hip_quant_mxfp4_dual(
             input.data_ptr(), input.size(0), input.size(1), row_q.data_ptr(), row_q.numel(), row_s.data_ptr(),
             row_s.numel(), col_q.data_ptr(), col_q.numel(), col_s.data_ptr(), col_s.numel(), float(eps), stream))
+
+
+# ---------------------------------------------------------------- payload rows
+# The expert-parallel payload row [codes (H/2 B) | E8M0 scales (H/32 B)] that
+# Megatron builds with torch.cat before the DeepEP dispatch and splits with
+# two .contiguous() copies after it (code/megatron-0.15.0rc7.diff:32-63,
+# 163-170). These entry points write and read it in place.
+def _payload_cols(packed: torch.Tensor) -> int:
+    width = packed.size(-1)
+    if width % 17 != 0:
+        raise RuntimeError(f"payload width {width} is not 17/16 of a code width")
+    return width // 17 * 32
+
+
+def omo_quant_mxfp4_packed(input, output, eps=1e-10):
+    """BF16 [T, H] -> payload rows [T, 17H/32] uint8, byte-identical to
+    torch.cat(quantize codes, quantize scales, dim=-1). H % 128 == 0."""
+    _check_input(input, "input")
+    _check_input(output, "output")
+    _same_device(input, output)
+    if input.dim() != 2:
+        raise RuntimeError("input must be 2-D")
+    _check_dtype(input, torch.bfloat16, "input")
+    _check_dtype(output, torch.uint8, "output")
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_quant_mxfp4_packed(input.data_ptr(), input.size(0), input.size(1), output.data_ptr(),
+                                               output.numel(), float(eps), stream))
+
+
+def omo_packed_Mxfp4ToBf16_dequant(input, output):
+    """Payload rows [T, 17H/32] -> bf16 [T, H]."""
+    _check_input(input, "input")
+    _check_input(output, "output")
+    _same_device(input, output)
+    if input.dim() != 2:
+        raise RuntimeError("input must be 2-D")
+    _check_dtype(input, torch.uint8, "input")
+    _check_dtype(output, torch.bfloat16, "output")
+    cols = _payload_cols(input)
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_packed_Mxfp4ToBf16_dequant(input.data_ptr(), input.size(0), cols, output.data_ptr(),
+                                                       output.numel(), stream))
+
+
+def omo_packed_Mxfp4ToFp8(input, output_q, output_s):
+    """Payload rows [T, 17H/32] -> fp8 [T, H] + fp32 [H/128, T], the outputs of
+    omo_per_token_Mxfp4ToFp8 on the unpacked codes and scales."""
+    for t, n in ((input, "input"), (output_q, "output_q"), (output_s, "output_s")):
+        _check_input(t, n)
+    _same_device(input, output_q, output_s)
+    if input.dim() != 2:
+        raise RuntimeError("input must be 2-D")
+    _check_dtype(input, torch.uint8, "input")
+    _check_dtype(output_q, _FP8, "output_q")
+    _check_dtype(output_s, torch.float32, "output_s")
+    cols = _payload_cols(input)
+    with _on_device(input) as stream:
+        _check(_lib.omo_hip_packed_Mxfp4ToFp8(input.data_ptr(), input.size(0), cols, output_q.data_ptr(),
+                                              output_q.numel(), output_s.data_ptr(), output_s.numel(), stream))

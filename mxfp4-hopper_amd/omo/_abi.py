@@ -29,6 +29,9 @@ SIGNATURES = {
     "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit": [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P,
                                                         _I64, _I64, _F, _P],
     "omo_hip_quant_mxfp4_dual": [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _F, _P],
+    "omo_hip_quant_mxfp4_packed": [_P, _I64, _I64, _P, _I64, _F, _P],
+    "omo_hip_packed_Mxfp4ToBf16_dequant": [_P, _I64, _I64, _P, _I64, _P],
+    "omo_hip_packed_Mxfp4ToFp8": [_P, _I64, _I64, _P, _I64, _P, _I64, _P],
 }
 
 

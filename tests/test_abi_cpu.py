@@ -24,6 +24,7 @@ def test_header_declares_the_reference_entry_points():
               "omo_hip_per_token_Mxfp4ToFp8", "omo_hip_per_token_Mxfp4ToBf16ToFp8",
               "omo_hip_per_token_Mxfp4ToFp8_col", "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col",
               "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit", "omo_hip_quant_mxfp4_dual",
+              "omo_hip_quant_mxfp4_packed", "omo_hip_packed_Mxfp4ToBf16_dequant", "omo_hip_packed_Mxfp4ToFp8",
               "omo_hip_abi_version", "omo_hip_status_string", "omo_hip_last_error"]:
         assert n in names
 
@@ -129,3 +130,41 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "exactly one GPU" in r.stdout
+
+
+def test_payload_validation_paths():
+    lib = _lib()
+    f = ctypes.c_void_p(0x1000)
+    # cols % 128 (payload rows must stay dword aligned)
+    assert lib.omo_hip_quant_mxfp4_packed(f, 2, 96, f, 2 * 51, 1e-10, None) == -1
+    assert b"multiple of 128" in lib.omo_hip_last_error()
+    # undersized output, misaligned input, non-finite eps
+    assert lib.omo_hip_quant_mxfp4_packed(f, 2, 128, f, 2 * 68 - 1, 1e-10, None) == -1
+    assert lib.omo_hip_quant_mxfp4_packed(ctypes.c_void_p(0x1008), 2, 128, f, 136, 1e-10, None) == -1
+    assert lib.omo_hip_quant_mxfp4_packed(f, 2, 128, f, 136, float("inf"), None) == -1
+    assert lib.omo_hip_packed_Mxfp4ToBf16_dequant(f, 2, 128, f, 255, None) == -1
+    assert lib.omo_hip_packed_Mxfp4ToBf16_dequant(ctypes.c_void_p(0x1002), 2, 128, f, 256, None) == -1
+    assert lib.omo_hip_packed_Mxfp4ToFp8(f, 2, 128, f, 256, f, 1, None) == -1
+    # empty payloads are no-op successes
+    assert lib.omo_hip_quant_mxfp4_packed(None, 0, 7168, None, 0, 1e-10, None) == 0
+    assert lib.omo_hip_packed_Mxfp4ToBf16_dequant(None, 0, 7168, None, 0, None) == 0
+    assert lib.omo_hip_packed_Mxfp4ToFp8(None, 0, 7168, None, 0, None, 0, None) == 0
+
+
+def test_payload_pack_unpack_like_megatron():
+    """pack/unpack keep Megatron's behaviour (megatron-0.15.0rc7.diff:93-122):
+    width * 16 / 17 split, contiguous parts, its errors."""
+    from omo_python_api.ep_payload import pack_rowwise_components, payload_width, unpack_rowwise_components
+    g = torch.Generator().manual_seed(3)
+    q = torch.randint(0, 256, (5, 3584), generator=g, dtype=torch.uint8)
+    s = torch.randint(0, 256, (5, 224), generator=g, dtype=torch.uint8)
+    p = pack_rowwise_components(q, s)
+    assert p.shape == (5, payload_width(7168)) == (5, 3808)
+    uq, us = unpack_rowwise_components(p)
+    assert torch.equal(uq, q) and torch.equal(us, s) and uq.is_contiguous() and us.is_contiguous()
+    with pytest.raises(ValueError, match="must match"):
+        pack_rowwise_components(q, s[:4])
+    with pytest.raises(ValueError, match="17/16"):
+        unpack_rowwise_components(torch.zeros((2, 100), dtype=torch.uint8))
+    with pytest.raises(ValueError, match="at least one dimension"):
+        unpack_rowwise_components(torch.zeros((), dtype=torch.uint8))

@@ -436,3 +436,58 @@ def test_dual_layout(oracle, dev, M, K, seed):
     eqt, est = oracle.quant_mxfp4(np.ascontiguousarray(xb.T).reshape(-1))
     np.testing.assert_array_equal(bits_u8(cq).reshape(-1), eqt)
     np.testing.assert_array_equal(bits_u8(cs).reshape(-1), est)
+
+
+# ------------------------------------------------- expert-parallel payload rows
+def _payload(codes, scales):
+    """Megatron's torch.cat of codes [T, H/2] and scales [T, H/32] (numpy)."""
+    T = codes.shape[0]
+    return np.ascontiguousarray(np.concatenate([codes.reshape(T, -1), scales.reshape(T, -1)], axis=1))
+
+
+@pytest.mark.parametrize("T,H,seed", [(1, 128, 1), (300, 7168, 2), (64, 2048, 3), (4, 128, 0), (0, 7168, 5)])
+def test_payload_quant(oracle, dev, T, H, seed):
+    """Quantize into payload rows == torch.cat of the unfused quantize outputs."""
+    from omo_python_api.ep_payload import fp4_quantize_packed, pack_rowwise_components
+    from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
+    _say("payload quant", T, H, seed)
+    if seed == 0:  # the special-value blocks (inf, NaN, denormals, ...) padded to whole rows
+        sb = special_blocks()
+        xb = np.zeros(T * H, np.uint16)
+        xb[: sb.size] = sb
+        x = from_u16(xb, "cpu").view(T, H)
+    else:
+        x = (torch.randn((T, H), generator=torch.Generator().manual_seed(seed)) * 3).to(torch.bfloat16)
+    xd = x.to(dev)
+    p = fp4_quantize_packed(xd)
+    q, s = omo_per_token_group_quant_mxfp4(xd)
+    torch.cuda.synchronize()
+    assert p.shape == (T, H // 2 + H // 32) and p.dtype == torch.uint8
+    assert torch.equal(p, pack_rowwise_components(q, s))
+    if T:
+        eq, es = oracle.quant_mxfp4(bits_u16(x).reshape(-1))
+        np.testing.assert_array_equal(bits_u8(p), _payload(eq.reshape(T, -1), es.reshape(T, -1)))
+
+
+@pytest.mark.parametrize("T,H,seed,spread", [(2, 128, 1, 16), (300, 7168, 2, 255), (64, 2048, 3, 8), (3, 256, 4, 3)])
+def test_payload_dequant_and_requant(oracle, dev, T, H, seed, spread):
+    """Dequant and FP8 requant of payload rows == the unfused kernels on the
+    unpacked codes and scales (oracle), including m_splits."""
+    from omo_python_api.ep_payload import packed_mxfp4ToBf16, packed_mxfp4ToFp8, unpack_rowwise_components
+    _say("payload dequant/requant", T, H, seed, spread)
+    q, s = scale_spread_payload(T, H // 2, seed, spread)
+    p = torch.from_numpy(_payload(q, s)).to(dev)
+    dq = packed_mxfp4ToBf16(p)
+    splits = [T // 3, 0, T - T // 3]
+    f8s, ss = packed_mxfp4ToFp8(p, splits)
+    f8, sc = packed_mxfp4ToFp8(p)
+    torch.cuda.synchronize()
+    uq, us = unpack_rowwise_components(p)
+    assert torch.equal(uq.cpu(), torch.from_numpy(q)) and torch.equal(us.cpu(), torch.from_numpy(s))
+    np.testing.assert_array_equal(bits_u16(dq).reshape(-1), oracle.dequant_bf16(q, s))
+    eo, es = oracle.mxfp4_to_fp8(q, s)
+    np.testing.assert_array_equal(bits_u8(f8), eo)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), es.view(np.uint32))
+    assert [t.shape[0] for t in f8s] == splits and [t.shape[1] for t in ss] == splits
+    np.testing.assert_array_equal(bits_u8(torch.cat(f8s)), eo)
+    np.testing.assert_array_equal(torch.cat(ss, 1).cpu().numpy().view(np.uint32), es.view(np.uint32))
