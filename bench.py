@@ -11,8 +11,9 @@ set. The script prints one JSON line.
 Also measured (extra keys): MXFP4 -> BF16 dequant of the same shape, the
 MoE-payload requant/dequant (4096 x 7168, both FP8 layouts), the fused
 expert-parallel payload rows against Megatron's cat/split composition, the
-dual-layout quantize (7168 x 18432) and the row -> col FP8 conversion, each as
-GB/s of algorithmic bytes or microseconds per call.
+cfg5 MoE layer composite (all codec launches of one layer on 8 local experts),
+the dual-layout quantize (7168 x 18432) and the row -> col FP8 conversion,
+each as GB/s of algorithmic bytes or microseconds per call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        [--only quant|dequant|...] [--copy-calibration]
@@ -38,7 +39,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (>= 3 to exceed the 256 MB cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of legs: quant,dequant,payload,ep_payload,dual,rowcol")
+    ap.add_argument("--only", default="", help="comma list of legs: quant,dequant,payload,ep_payload,moe,dual,rowcol")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (known traffic) for counter calibration")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -57,6 +58,18 @@ def sleep_gpu(torch, ms=5.0):
 
 
 GRAPH = True
+
+
+def _split_meta(m_splits):
+    """Exclusive prefix sums of the grouped row -> col kernel: (lens, row
+    offsets, scale-row offsets, max split length)."""
+    offs, soffs, o, so = [], [], 0, 0
+    for m in m_splits:
+        offs.append(o)
+        soffs.append(so)
+        o += m
+        so += -(-m // 128)
+    return list(m_splits), offs, soffs, max(m_splits) if m_splits else 0
 
 
 def sets_for(bytes_per_set, minimum):
@@ -296,6 +309,59 @@ def main():
             "recv_fp8_fused_GB/s": round(wl.requant_fp8_bytes(n5) / (res["recv_fp8_fused"] * 1e-6) / 1e9, 1),
         }
         del xe, pe
+
+    if want("moe"):
+        # cfg5: one MoE layer's MXFP4 codec work on the GPU that owns experts 0-7 of 64
+        # (16384 tokens, top-8 of 64, seeded): per-expert rows m_e (ragged, ~2048 each),
+        # concatenated [R = sum m_e] where rows are independent.
+        c5 = wl.CFG5
+        m_e = wl.moe_routing(c5["tokens"], c5["n_experts"], c5["topk"], range(c5["local_experts"]), seed=5)
+        R, Hd, Fd = sum(m_e), c5["hidden"], c5["ffn"]
+        rows_t = [(R, Hd), (R, Fd), (R, Hd), (R, 2 * Fd)]  # fwd act, fc2 input, bwd grads (fc2, fc1)
+        xq = [wl.normal_bf16(sh, seed=70 + i, device=dev) for i, sh in enumerate(rows_t)]
+        oq = [(torch.empty((r, c // 2), dtype=torch.uint8, device=dev), torch.empty((r, c // 32), dtype=torch.uint8,
+                                                                                   device=dev)) for r, c in rows_t]
+        w_shapes = [(Hd, Fd), (Hd, Fd), (Fd, Hd)] * c5["local_experts"]  # gate, up, down per expert
+        ws = [wl.normal_bf16(sh, seed=100 + i, device=dev, std=0.02) for i, sh in enumerate(w_shapes)]
+        wo = [tuple(torch.empty(shp, dtype=torch.uint8, device=dev)
+                    for shp in ((r, c // 2), (r, c // 32), (c, r // 2), (c, r // 32))) for r, c in w_shapes]
+        # wgrad: per-split row -> col FP8 of the activation codes
+        lens5, offs5, soffs5, mx5 = (torch.tensor(v, dtype=torch.int32, device=dev) if i < 3 else v
+                                     for i, v in enumerate(_split_meta(m_e)))
+        srows5 = sum(-(-m // 128) for m in m_e)
+        rc_out = torch.empty((R * Hd,), dtype=torch.uint8, device=dev)
+        rc_s = torch.empty((srows5, Hd), dtype=torch.float32, device=dev)
+
+        def moe_step(_i):
+            for (x, (q, s)) in zip(xq, oq):
+                n_ = x.numel()
+                _abi.check(lib.omo_hip_per_token_group_quant_fp4(x.data_ptr(), n_, q.data_ptr(), n_ // 2, s.data_ptr(),
+                                                                 n_ // 32, 32, 1e-10, -6.0, 6.0, 0, cur()))
+            for w, (rq_, rs_, cq_, cs_) in zip(ws, wo):
+                n_ = w.numel()
+                _abi.check(lib.omo_hip_quant_mxfp4_dual(w.data_ptr(), w.size(0), w.size(1), rq_.data_ptr(), n_ // 2,
+                                                        rs_.data_ptr(), n_ // 32, cq_.data_ptr(), n_ // 2,
+                                                        cs_.data_ptr(), n_ // 32, 1e-10, cur()))
+            q0, s0 = oq[0]
+            _abi.check(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(
+                q0.data_ptr(), R, Hd // 2, s0.data_ptr(), s0.numel(), rc_out.data_ptr(), rc_out.numel(),
+                rc_s.data_ptr(), rc_s.numel(), lens5.data_ptr(), offs5.data_ptr(), soffs5.data_ptr(), len(m_e), mx5,
+                1e-10, cur()))
+
+        moe_bytes = (sum(wl.quant_bytes(r * c) for r, c in rows_t) + sum(wl.dual_quant_bytes(r * c) for r, c in w_shapes)
+                     + sum(wl.row_to_col_fp8_bytes(m, Hd) for m in m_e))
+        steps = max(10, args.steps // 50)
+        t, _ = time_launches(torch, moe_step, 1, steps, 2)
+        out["moe_cfg5"] = {
+            "workload": f"cfg5 MoE layer on experts 0-7 of 64: 16384 tokens top-8, R={R} local rows "
+                        f"(m_e {min(m_e)}..{max(m_e)}); 4 activation/grad quantizes, 24 weight dual quantizes, "
+                        "per-split row->col FP8",
+            "launches_per_step": len(rows_t) + len(w_shapes) + 1,
+            "algorithmic_bytes_per_step": moe_bytes,
+            "us_per_step": round(t / steps * 1e3, 1),
+            "GB/s": round(moe_bytes / (t / steps * 1e-3) / 1e9, 1),
+        }
+        del xq, oq, ws, wo, rc_out, rc_s
 
     if want("dual"):
         Mw, Kw = 7168, 18432

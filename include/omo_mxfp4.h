@@ -168,6 +168,31 @@ OMO_API int omo_hip_packed_Mxfp4ToBf16_dequant(const void* input, int64_t rows, 
 OMO_API int omo_hip_packed_Mxfp4ToFp8(const void* input, int64_t rows, int64_t cols, void* output_q,
                                       int64_t output_q_bytes, void* output_s, int64_t output_s_elems, void* stream);
 
+/* MXFP4 row permutation: the data movement of TE's moe_permute for MXFP4
+ * inputs (code/transformer_engine-2.8.diff:256-261, 338-354), which permutes
+ * the code rows [T, cols/2] and scale rows [T, cols/32] into expert-major
+ * order. Output row r of out_codes [num_out, cols/2] and out_scales
+ * [num_out, cols/32] is input row src_rows[r] (int32 device array, num_out
+ * entries); an index outside [0, num_tokens) gives a zero row. Input rows
+ * are code_stride / scale_stride bytes apart (payload rows can be read in
+ * place); codes_bytes / scales_bytes bound the input buffers. cols % 32 == 0. */
+OMO_API int omo_hip_mxfp4_permute_rows(const void* codes, int64_t codes_bytes, int64_t code_stride,
+                                       const void* scales, int64_t scales_bytes, int64_t scale_stride,
+                                       int64_t num_tokens, int64_t cols, const int32_t* src_rows, int64_t num_out,
+                                       void* out_codes, int64_t out_codes_bytes, void* out_scales,
+                                       int64_t out_scales_bytes, void* stream);
+
+/* The permutation fused with the FP8 E4M3 rowwise requant: output_q
+ * [num_out, cols] fp8 (16-byte aligned) and output_s [cols/128, num_out]
+ * fp32 equal omo_per_token_Mxfp4ToFp8 (code/kernel/per_token_Mxfp4ToFp8.cu:86-309)
+ * applied to the permuted rows, zero rows included. cols % 128 == 0; code and
+ * scale rows 4-byte aligned. */
+OMO_API int omo_hip_permute_Mxfp4ToFp8(const void* codes, int64_t codes_bytes, int64_t code_stride,
+                                       const void* scales, int64_t scales_bytes, int64_t scale_stride,
+                                       int64_t num_tokens, int64_t cols, const int32_t* src_rows, int64_t num_out,
+                                       void* output_q, int64_t output_q_bytes, void* output_s,
+                                       int64_t output_s_elems, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,24 @@ int check_packed(const char* fn, int64_t rows, int64_t cols) {
   return OMO_OK;
 }
 
+// Shared checks of the permutation entry points: strided input rows of codes
+// and scales, num_out int32 source indices.
+int check_permute(const char* fn, const void* codes, int64_t codes_bytes, int64_t code_stride, const void* scales,
+                  int64_t scales_bytes, int64_t scale_stride, int64_t num_tokens, int64_t cols,
+                  const int32_t* src_rows, int64_t num_out) {
+  REQUIRE(num_tokens >= 0 && cols >= 0 && num_out >= 0, "%s: negative shape", fn);
+  REQUIRE(cols % 32 == 0, "%s: cols must be a multiple of 32 (got %lld)", fn, (long long)cols);
+  REQUIRE(num_tokens < ((int64_t)1 << 31) && num_out < ((int64_t)1 << 31), "%s: too many rows", fn);
+  REQUIRE(code_stride >= cols / 2 && scale_stride >= cols / 32, "%s: row stride shorter than the row", fn);
+  const int64_t code_need = num_tokens == 0 ? 0 : (num_tokens - 1) * code_stride + cols / 2;
+  const int64_t scale_need = num_tokens == 0 ? 0 : (num_tokens - 1) * scale_stride + cols / 32;
+  REQUIRE_BUF("codes", codes, codes_bytes, code_need);
+  REQUIRE_BUF("scales", scales, scales_bytes, scale_need);
+  REQUIRE(num_out == 0 || src_rows != nullptr, "%s: src_rows: null pointer", fn);
+  REQUIRE(aligned(src_rows, 4), "%s: src_rows must be 4-byte aligned", fn);
+  return OMO_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -307,8 +325,48 @@ int omo_hip_packed_Mxfp4ToFp8(const void* input, int64_t rows, int64_t cols, voi
           "%s: input needs 4-byte, output_q 16-byte, output_s 4-byte alignment", fn);
   if (rows == 0 || cols == 0) return ok();
   const uint8_t* in = static_cast<const uint8_t*>(input);
-  return from_hip(omo_hip::launch_mxfp4_to_fp8_rows(in, stride, in + cols / 2, stride, output_q,
+  return from_hip(omo_hip::launch_mxfp4_to_fp8_rows(in, stride, in + cols / 2, stride, nullptr, rows, output_q,
                                                     static_cast<float*>(output_s), rows, cols / 2,
+                                                    as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_mxfp4_permute_rows(const void* codes, int64_t codes_bytes, int64_t code_stride, const void* scales,
+                               int64_t scales_bytes, int64_t scale_stride, int64_t num_tokens, int64_t cols,
+                               const int32_t* src_rows, int64_t num_out, void* out_codes, int64_t out_codes_bytes,
+                               void* out_scales, int64_t out_scales_bytes, void* stream) {
+  const char* fn = "omo_mxfp4_permute_rows";
+  int rc = check_permute(fn, codes, codes_bytes, code_stride, scales, scales_bytes, scale_stride, num_tokens, cols,
+                         src_rows, num_out);
+  if (rc != OMO_OK) return rc;
+  REQUIRE_BUF("out_codes", out_codes, out_codes_bytes, num_out * (cols / 2));
+  REQUIRE_BUF("out_scales", out_scales, out_scales_bytes, num_out * (cols / 32));
+  if (num_out == 0 || cols == 0) return ok();
+  return from_hip(omo_hip::launch_gather_rows(codes, code_stride, cols / 2, scales, scale_stride, cols / 32,
+                                              src_rows, num_tokens, num_out, out_codes, out_scales,
+                                              as_stream(stream)),
+                  fn);
+}
+
+int omo_hip_permute_Mxfp4ToFp8(const void* codes, int64_t codes_bytes, int64_t code_stride, const void* scales,
+                               int64_t scales_bytes, int64_t scale_stride, int64_t num_tokens, int64_t cols,
+                               const int32_t* src_rows, int64_t num_out, void* output_q, int64_t output_q_bytes,
+                               void* output_s, int64_t output_s_elems, void* stream) {
+  const char* fn = "omo_permute_Mxfp4ToFp8";
+  int rc = check_permute(fn, codes, codes_bytes, code_stride, scales, scales_bytes, scale_stride, num_tokens, cols,
+                         src_rows, num_out);
+  if (rc != OMO_OK) return rc;
+  REQUIRE(cols % 128 == 0, "%s: cols must be a multiple of 128 (got %lld)", fn, (long long)cols);
+  REQUIRE(code_stride % 4 == 0 && scale_stride % 4 == 0 && aligned(codes, 4) && aligned(scales, 4),
+          "%s: code and scale rows must be 4-byte aligned", fn);
+  REQUIRE(cols / 128 * num_out < ((int64_t)1 << 31), "%s: too many groups", fn);
+  REQUIRE_BUF("output_q", output_q, output_q_bytes, num_out * cols);
+  REQUIRE_BUF("output_s", output_s, output_s_elems, num_out * (cols / 128));
+  REQUIRE(aligned(output_q, 16) && aligned(output_s, 4), "%s: output_q needs 16-byte, output_s 4-byte alignment",
+          fn);
+  if (num_out == 0 || cols == 0) return ok();
+  return from_hip(omo_hip::launch_mxfp4_to_fp8_rows(codes, code_stride, scales, scale_stride, src_rows, num_tokens,
+                                                    output_q, static_cast<float*>(output_s), num_out, cols / 2,
                                                     as_stream(stream)),
                   fn);
 }

@@ -34,8 +34,18 @@ hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, 
 hipError_t launch_dequant_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride, void* out,
                                int64_t rows, int64_t K, hipStream_t stream);
 
-hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride, void* out,
-                                    float* out_s, int64_t M, int64_t Kb, hipStream_t stream);
+// src: optional int32 source row per output row (indices outside [0, n_src)
+// read zeros); M output rows.
+hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride,
+                                    const int32_t* src, int64_t n_src, void* out, float* out_s, int64_t M, int64_t Kb,
+                                    hipStream_t stream);
+
+// Gather rows of two byte tensors (codes and scales of MXFP4 rows) into
+// contiguous outputs: out row r = input row src[r]; zeros for indices
+// outside [0, n_src).
+hipError_t launch_gather_rows(const void* a, int64_t a_stride, int64_t a_bytes, const void* b, int64_t b_stride,
+                              int64_t b_bytes, const int32_t* src, int64_t n_src, int64_t n_out, void* out_a,
+                              void* out_b, hipStream_t stream);
 
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
                              float eps, hipStream_t stream);

@@ -1,0 +1,70 @@
+// Row gather of MXFP4 tensors: the data movement of TE's moe_permute for
+// MXFP4 inputs (code/transformer_engine-2.8.diff:256-261, 338-354), which
+// permutes the code rows [T, H/2] and the scale rows [T, H/32] of the tokens
+// into expert-major order with TE's own row permutation kernel.
+//
+// Output row r of both tensors is input row src[r]; an index outside
+// [0, n_src) writes a zero row (the padding rows of a permutation with more
+// output rows than routed tokens). Inputs may be strided (bytes between rows),
+// so the expert-parallel payload rows [codes | scales] are read in place.
+//
+// One wave per output row, 4 rows per 256-thread workgroup; each lane moves
+// V-sized pieces (16 B when every row start and row length allows it).
+#include "omo_device.cuh"
+#include "omo_internal.h"
+
+namespace omo_hip {
+
+template <typename V>
+__device__ __forceinline__ void copy_row(const uint8_t* __restrict__ in, bool ok, uint8_t* __restrict__ out,
+                                         int64_t bytes, int lane) {
+  const int64_t n = bytes / (int64_t)sizeof(V);
+  const V* src = reinterpret_cast<const V*>(in);
+  V* dst = reinterpret_cast<V*>(out);
+  V zero;
+  memset(&zero, 0, sizeof(V));
+  for (int64_t i = lane; i < n; i += 64) dst[i] = ok ? __builtin_nontemporal_load(src + i) : zero;
+}
+
+template <typename V>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint8_t* __restrict__ a, int64_t a_stride,
+                                                          int64_t a_bytes, const uint8_t* __restrict__ b,
+                                                          int64_t b_stride, int64_t b_bytes,
+                                                          const int32_t* __restrict__ src, int64_t n_src,
+                                                          int64_t n_out, uint8_t* __restrict__ out_a,
+                                                          uint8_t* __restrict__ out_b) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= n_out) return;
+  const int lane = (int)(threadIdx.x & 63);
+  const int64_t sr = src[r];
+  const bool ok = sr >= 0 && sr < n_src;
+  const int64_t rr = ok ? sr : 0;
+  copy_row<V>(a + rr * a_stride, ok, out_a + r * a_bytes, a_bytes, lane);
+  copy_row<V>(b + rr * b_stride, ok, out_b + r * b_bytes, b_bytes, lane);
+}
+
+hipError_t launch_gather_rows(const void* a, int64_t a_stride, int64_t a_bytes, const void* b, int64_t b_stride,
+                              int64_t b_bytes, const int32_t* src, int64_t n_src, int64_t n_out, void* out_a,
+                              void* out_b, hipStream_t stream) {
+  if (n_out == 0) return hipSuccess;
+  // widest piece dividing every row start and row length
+  const uint64_t bits = (uint64_t)a_stride | (uint64_t)a_bytes | (uint64_t)b_stride | (uint64_t)b_bytes |
+                        reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                        reinterpret_cast<uintptr_t>(out_a) | reinterpret_cast<uintptr_t>(out_b);
+  const dim3 grid((unsigned)((n_out + 3) / 4)), block(256);
+  const uint8_t *pa = static_cast<const uint8_t*>(a), *pb = static_cast<const uint8_t*>(b);
+  uint8_t *qa = static_cast<uint8_t*>(out_a), *qb = static_cast<uint8_t*>(out_b);
+  if ((bits & 15) == 0) {
+    hipLaunchKernelGGL(gather_rows_kernel<u32x4>, grid, block, 0, stream, pa, a_stride, a_bytes, pb, b_stride,
+                       b_bytes, src, n_src, n_out, qa, qb);
+  } else if ((bits & 3) == 0) {
+    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, grid, block, 0, stream, pa, a_stride, a_bytes, pb, b_stride,
+                       b_bytes, src, n_src, n_out, qa, qb);
+  } else {
+    hipLaunchKernelGGL(gather_rows_kernel<uint8_t>, grid, block, 0, stream, pa, a_stride, a_bytes, pb, b_stride,
+                       b_bytes, src, n_src, n_out, qa, qb);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace omo_hip

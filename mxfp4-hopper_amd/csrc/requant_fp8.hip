@@ -88,9 +88,14 @@ constexpr int kRqRows = 32;
 // s + r * s_stride (bytes): contiguous [M, Kb] + [M, Kb/16] tensors, or the
 // expert-parallel payload rows [codes | scales] read in place. ALIGN8: the
 // code rows are 8-byte aligned (one 8 B load per lane, else two 4 B loads).
+// src (optional): output row r reads input row src[r] (a gather, e.g. the
+// expert-major token order of a MoE permutation); an index outside
+// [0, n_src) reads zero codes and zero scale bytes, i.e. the row a permutation
+// pads with zeros, requantized.
 template <int UNROLL, bool ALIGN8>
 __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __restrict__ q, int64_t q_stride,
                                                            const uint8_t* __restrict__ s, int64_t s_stride,
+                                                           const int32_t* __restrict__ src, int64_t n_src,
                                                            u32x4* __restrict__ out, float* __restrict__ out_s,
                                                            uint32_t M, uint32_t gpr, uint32_t gx) {
   constexpr int PPR = 8 * kRqGroups;  // pairs per tile row
@@ -104,14 +109,21 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
     const int e = u * 256 + threadIdx.x;
     const uint32_t r = by * kRqRows + e / PPR, cp = bx * PPR + e % PPR;
     if (r < M && cp < 8 * gpr) {
-      const uint8_t* src = q + r * q_stride + 8 * (int64_t)cp;
-      if (ALIGN8) {
-        c[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
+      const int64_t sr = src ? (int64_t)src[r] : (int64_t)r;
+      if (sr >= 0 && sr < n_src) {
+        const uint8_t* p = q + sr * q_stride + 8 * (int64_t)cp;
+        if (ALIGN8) {
+          c[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        } else {
+          c[u][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+          c[u][1] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p + 4));
+        }
+        sd[u] = *reinterpret_cast<const uint32_t*>(s + sr * s_stride + 4 * (cp >> 3));
       } else {
-        c[u][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
-        c[u][1] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + 4));
+        c[u][0] = 0u;
+        c[u][1] = 0u;
+        sd[u] = 0u;
       }
-      sd[u] = *reinterpret_cast<const uint32_t*>(s + r * s_stride + 4 * (cp >> 3));
     }
   }
 #pragma unroll
@@ -145,8 +157,9 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
   }
 }
 
-hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride, void* out,
-                                    float* out_s, int64_t M, int64_t Kb, hipStream_t stream) {
+hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void* s, int64_t s_stride,
+                                    const int32_t* src, int64_t n_src, void* out, float* out_s, int64_t M, int64_t Kb,
+                                    hipStream_t stream) {
   if (M == 0 || Kb == 0) return hipSuccess;
   constexpr int U = kRqRows * 8 * kRqGroups / 256;
   const int64_t gpr = Kb / 64;
@@ -154,14 +167,14 @@ hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void*
   const bool a8 = (q_stride % 8 == 0) && ((reinterpret_cast<uintptr_t>(q) & 7) == 0);
   auto kernel = a8 ? mxfp4_to_fp8_kernel<U, true> : mxfp4_to_fp8_kernel<U, false>;
   hipLaunchKernelGGL(kernel, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q), q_stride,
-                     static_cast<const uint8_t*>(s), s_stride, static_cast<u32x4*>(out), out_s, (uint32_t)M,
-                     (uint32_t)gpr, (uint32_t)gx);
+                     static_cast<const uint8_t*>(s), s_stride, src, n_src, static_cast<u32x4*>(out), out_s,
+                     (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
   return hipGetLastError();
 }
 
 hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
                                hipStream_t stream) {
-  return launch_mxfp4_to_fp8_rows(q, Kb, s, Kb / 16, out, out_s, M, Kb, stream);
+  return launch_mxfp4_to_fp8_rows(q, Kb, s, Kb / 16, nullptr, M, out, out_s, M, Kb, stream);
 }
 
 // ------------------------------------------------------------ transposed

@@ -350,11 +350,54 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_kernel(const uint8_
   }
 }
 
+// Bytes [lo, hi) of a 16 B block at a 16 B aligned address, in pieces of 8,
+// 4, 2 and 1 bytes at their natural alignment (at most 6 pieces).
+__device__ __forceinline__ void store_partial16(uint8_t* __restrict__ dst, const u32x4& v, int lo, int hi) {
+  int k = lo;
+#pragma unroll
+  for (int it = 0; it < 7; it++) {
+    if (k >= hi) break;
+    const uint32_t w0 = k < 4 ? v[0] : k < 8 ? v[1] : k < 12 ? v[2] : v[3];
+    if ((k & 7) == 0 && k + 8 <= hi) {
+      u32x2 w;
+      w[0] = w0;
+      w[1] = k < 4 ? v[1] : v[3];
+      *reinterpret_cast<u32x2*>(dst + k) = w;
+      k += 8;
+    } else if ((k & 3) == 0 && k + 4 <= hi) {
+      *reinterpret_cast<uint32_t*>(dst + k) = w0;
+      k += 4;
+    } else if ((k & 1) == 0 && k + 2 <= hi) {
+      *reinterpret_cast<uint16_t*>(dst + k) = (uint16_t)(w0 >> (8 * (k & 3)));
+      k += 2;
+    } else {
+      dst[k] = (uint8_t)(w0 >> (8 * (k & 3)));
+      k += 1;
+    }
+  }
+}
+
+// LDS bytes per staged output column: 16 B of padding on each side of the
+// tile's 128 rows, so shifted 16 B windows stay inside the row.
+constexpr int kOutPitch = 16 + kTile + 16;
+
+struct MsplitSmem {
+  RowColSmem rc;
+  uint8_t obuf[kTile][kOutPitch];
+};
+
+// A split's output column c is a run of len bytes at off*N + c*len, so the
+// tile's 128-row piece of a column starts at an arbitrary byte alignment.
+// The tile's output columns are staged in LDS; lane q of a column then
+// writes the q-th 16 B aligned block of the column's piece (lane 0 also the
+// ninth), taking the bytes from LDS with v_alignbyte_b32 over five dwords.
+// Full blocks are single 16 B stores; only the first and last block of a
+// piece are written in smaller pieces.
 __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
     int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs) {
-  __shared__ RowColSmem sm;
+  __shared__ __attribute__((aligned(16))) MsplitSmem sm;
   const int64_t split = blockIdx.x, bm = blockIdx.y, bn = blockIdx.z;
   const int64_t len = lens[split];
   if (bm * kTile >= len) return;
@@ -364,18 +407,52 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
   if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
   const int64_t row0 = start + bm * kTile, col0 = bn * kTile;
   const int rows_valid = (int)(len - bm * kTile < kTile ? len - bm * kTile : kTile);
-  rc_put(sm, rc_load(q, s, N, row0, rows_valid, col0, vin, vs));
+  rc_put(sm.rc, rc_load(q, s, N, row0, rows_valid, col0, vin, vs));
   __syncthreads();
   LaneCols res;
-  rc_tile<true>(sm, rows_valid, N, col0, 0.0f, eps, out_s + (sstart + bm) * N + col0, res);
+  rc_tile<true>(sm.rc, rows_valid, N, col0, 0.0f, eps, out_s + (sstart + bm) * N + col0, res);
   const int t = threadIdx.x, p = t >> 3, qq = t & 7;
-  const int64_t c = col0 + 2 * p;
-  if (c < N) {
-    const int64_t o0 = start * N + c * len + bm * kTile + 16 * qq;
-    const int64_t o1 = o0 + len;
-    const bool base_al = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-    rc_store(out + o0, res.e0, 16 * qq, rows_valid, base_al && (o0 & 15) == 0);
-    rc_store(out + o1, res.e1, 16 * qq, rows_valid, base_al && (o1 & 15) == 0);
+  // every piece of this split is 16 B aligned when len and N are multiples of
+  // 16 and out is aligned: each lane stores its own 16 B (uniform per workgroup)
+  if (len % 16 == 0 && N % 16 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    const int64_t c = col0 + 2 * p;
+    if (c < N) {
+      const int64_t o0 = start * N + c * len + bm * kTile + 16 * qq;
+      rc_store(out + o0, res.e0, 16 * qq, rows_valid, true);
+      rc_store(out + o0 + len, res.e1, 16 * qq, rows_valid, true);
+    }
+    return;
+  }
+  *reinterpret_cast<u32x4*>(&sm.obuf[2 * p][16 + 16 * qq]) = res.e0;
+  *reinterpret_cast<u32x4*>(&sm.obuf[2 * p + 1][16 + 16 * qq]) = res.e1;
+  __syncthreads();
+  if (col0 + 2 * p >= N) return;  // N is even: both columns or neither
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int c = 2 * p + h;
+    const int64_t o = start * N + (col0 + c) * len + bm * kTile;  // this tile's piece of column c
+    const int sft = (int)((reinterpret_cast<uintptr_t>(out) + (uintptr_t)o) & 15u);
+    uint8_t* a16 = out + o - sft;
+#pragma unroll
+    for (int j = qq; j <= 8; j += 8) {
+      const int lo = max(0, sft - 16 * j), hi = min(16, rows_valid + sft - 16 * j);
+      if (lo >= hi) continue;
+      // dest block j holds piece bytes [16 j - sft, 16 j - sft + 16)
+      const int b = 16 + 16 * j - sft;
+      const uint32_t* dw = reinterpret_cast<const uint32_t*>(&sm.obuf[c][b & ~3]);
+      const uint32_t sh = (uint32_t)(b & 3);
+      const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2], d3 = dw[3], d4 = dw[4];
+      u32x4 blk;
+      blk[0] = __builtin_amdgcn_alignbyte(d1, d0, sh);
+      blk[1] = __builtin_amdgcn_alignbyte(d2, d1, sh);
+      blk[2] = __builtin_amdgcn_alignbyte(d3, d2, sh);
+      blk[3] = __builtin_amdgcn_alignbyte(d4, d3, sh);
+      if (lo == 0 && hi == 16) {
+        *reinterpret_cast<u32x4*>(a16 + 16 * j) = blk;
+      } else {
+        store_partial16(a16 + 16 * j, blk, lo, hi);
+      }
+    }
   }
 }
 

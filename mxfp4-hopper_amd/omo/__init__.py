@@ -40,6 +40,8 @@ __all__ = [
     "omo_quant_mxfp4_packed",
     "omo_packed_Mxfp4ToBf16_dequant",
     "omo_packed_Mxfp4ToFp8",
+    "omo_mxfp4_permute_rows",
+    "omo_permute_Mxfp4ToFp8",
 ]
 
 _FP8 = torch.float8_e4m3fn
@@ -319,3 +321,61 @@ def omo_packed_Mxfp4ToFp8(input, output_q, output_s):
     with _on_device(input) as stream:
         _check(_lib.omo_hip_packed_Mxfp4ToFp8(input.data_ptr(), input.size(0), cols, output_q.data_ptr(),
                                               output_q.numel(), output_s.data_ptr(), output_s.numel(), stream))
+
+
+# ----------------------------------------------------------------- permutation
+# Row gathers of MXFP4 tensors (the data movement of TE's moe_permute for
+# MXFP4 inputs, code/transformer_engine-2.8.diff:256-261, 338-354). codes
+# [T, H/2] and scales [T, H/32] may be row-strided views (last-dim stride 1),
+# e.g. the two halves of payload rows.
+def _rows_view(t: torch.Tensor, name: str):
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if t.dim() != 2 or (t.size(1) > 1 and t.stride(1) != 1):
+        raise RuntimeError(f"{name} must be 2-D with unit stride along the last dimension")
+    _check_dtype(t, torch.uint8, name)
+    rows = t.size(0)
+    stride = t.stride(0) if rows > 1 else t.size(1)
+    span = 0 if rows == 0 else (rows - 1) * stride + t.size(1)
+    return t.data_ptr(), span, stride
+
+
+def _permute_args(codes, scales, src_rows):
+    if codes.size(0) != scales.size(0):
+        raise RuntimeError("codes and scales must have the same number of rows")
+    cols = codes.size(1) * 2
+    if scales.size(1) != cols // 32:
+        raise RuntimeError("scales must have H/32 columns for codes of H/2 columns")
+    _check_input(src_rows, "src_rows")
+    _check_dtype(src_rows, torch.int32, "src_rows")
+    _same_device(codes, scales, src_rows)
+    cp, cb, cs = _rows_view(codes, "codes")
+    sp, sb, ss = _rows_view(scales, "scales")
+    return (cp, cb, cs, sp, sb, ss, codes.size(0), cols, src_rows.data_ptr(), src_rows.numel())
+
+
+def omo_mxfp4_permute_rows(codes, scales, src_rows, out_codes, out_scales):
+    """out_codes[r] = codes[src_rows[r]], out_scales[r] = scales[src_rows[r]]
+    (zero rows for indices outside [0, T))."""
+    args = _permute_args(codes, scales, src_rows)
+    for t, n in ((out_codes, "out_codes"), (out_scales, "out_scales")):
+        _check_input(t, n)
+        _check_dtype(t, torch.uint8, n)
+    _same_device(codes, out_codes, out_scales)
+    with _on_device(codes) as stream:
+        _check(_lib.omo_hip_mxfp4_permute_rows(*args, out_codes.data_ptr(), out_codes.numel(),
+                                               out_scales.data_ptr(), out_scales.numel(), stream))
+
+
+def omo_permute_Mxfp4ToFp8(codes, scales, src_rows, output_q, output_s):
+    """omo_per_token_Mxfp4ToFp8 of the gathered rows in one kernel: output_q
+    [N, H] fp8, output_s [H/128, N] fp32, N = src_rows.numel()."""
+    args = _permute_args(codes, scales, src_rows)
+    _check_input(output_q, "output_q")
+    _check_input(output_s, "output_s")
+    _check_dtype(output_q, _FP8, "output_q")
+    _check_dtype(output_s, torch.float32, "output_s")
+    _same_device(codes, output_q, output_s)
+    with _on_device(codes) as stream:
+        _check(_lib.omo_hip_permute_Mxfp4ToFp8(*args, output_q.data_ptr(), output_q.numel(), output_s.data_ptr(),
+                                               output_s.numel(), stream))

@@ -32,6 +32,8 @@ SIGNATURES = {
     "omo_hip_quant_mxfp4_packed": [_P, _I64, _I64, _P, _I64, _F, _P],
     "omo_hip_packed_Mxfp4ToBf16_dequant": [_P, _I64, _I64, _P, _I64, _P],
     "omo_hip_packed_Mxfp4ToFp8": [_P, _I64, _I64, _P, _I64, _P, _I64, _P],
+    "omo_hip_mxfp4_permute_rows": [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
+    "omo_hip_permute_Mxfp4ToFp8": [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
 }
 
 

@@ -25,6 +25,7 @@ def test_header_declares_the_reference_entry_points():
               "omo_hip_per_token_Mxfp4ToFp8_col", "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col",
               "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit", "omo_hip_quant_mxfp4_dual",
               "omo_hip_quant_mxfp4_packed", "omo_hip_packed_Mxfp4ToBf16_dequant", "omo_hip_packed_Mxfp4ToFp8",
+              "omo_hip_mxfp4_permute_rows", "omo_hip_permute_Mxfp4ToFp8",
               "omo_hip_abi_version", "omo_hip_status_string", "omo_hip_last_error"]:
         assert n in names
 
@@ -168,3 +169,37 @@ def test_payload_pack_unpack_like_megatron():
         unpack_rowwise_components(torch.zeros((2, 100), dtype=torch.uint8))
     with pytest.raises(ValueError, match="at least one dimension"):
         unpack_rowwise_components(torch.zeros((), dtype=torch.uint8))
+
+
+def test_make_row_id_map_expert_major():
+    """Routed (token, expert) pairs in expert-major order, tokens ascending
+    within an expert; padding rows -1; dest is the inverse map."""
+    from omo_python_api.permutation import make_row_id_map
+    rm = torch.tensor([[1, 0, 1],
+                       [0, 1, 1],
+                       [1, 1, 0],
+                       [0, 0, 0]], dtype=torch.bool)
+    src, m_splits, dest = make_row_id_map(rm, num_out_tokens=8)
+    assert m_splits == [2, 2, 2]
+    assert src.tolist() == [0, 2, 1, 2, 0, 1, -1, -1]
+    assert dest.tolist() == [[0, -1, 4], [-1, 2, 5], [1, 3, -1], [-1, -1, -1]]
+    with pytest.raises(ValueError):
+        make_row_id_map(rm, num_out_tokens=5)
+
+
+def test_permute_validation_paths():
+    lib = _lib()
+    f = ctypes.c_void_p(0x1000)
+    # cols % 32; stride shorter than the row; undersized input; null indices
+    assert lib.omo_hip_mxfp4_permute_rows(f, 1 << 20, 24, f, 1 << 20, 2, 4, 48, f, 4, f, 96, f, 8, None) == -1
+    assert lib.omo_hip_mxfp4_permute_rows(f, 1 << 20, 32, f, 1 << 20, 4, 4, 128, f, 4, f, 256, f, 16, None) == -1
+    assert lib.omo_hip_mxfp4_permute_rows(f, 100, 64, f, 1 << 20, 4, 4, 128, f, 4, f, 256, f, 16, None) == -1
+    assert lib.omo_hip_mxfp4_permute_rows(f, 1 << 20, 64, f, 1 << 20, 4, 4, 128, None, 4, f, 256, f, 16,
+                                          None) == -1
+    # fused fp8: cols % 128, 4-byte rows, output size
+    assert lib.omo_hip_permute_Mxfp4ToFp8(f, 1 << 20, 48, f, 1 << 20, 3, 4, 96, f, 4, f, 384, f, 4, None) == -1
+    assert lib.omo_hip_permute_Mxfp4ToFp8(f, 1 << 20, 66, f, 1 << 20, 4, 4, 128, f, 4, f, 512, f, 4, None) == -1
+    assert lib.omo_hip_permute_Mxfp4ToFp8(f, 1 << 20, 64, f, 1 << 20, 4, 4, 128, f, 4, f, 511, f, 4, None) == -1
+    # nothing to do
+    assert lib.omo_hip_permute_Mxfp4ToFp8(f, 1 << 20, 64, f, 1 << 20, 4, 4, 128, None, 0, None, 0, None, 0,
+                                          None) == 0

@@ -491,3 +491,57 @@ def test_payload_dequant_and_requant(oracle, dev, T, H, seed, spread):
     assert [t.shape[0] for t in f8s] == splits and [t.shape[1] for t in ss] == splits
     np.testing.assert_array_equal(bits_u8(torch.cat(f8s)), eo)
     np.testing.assert_array_equal(torch.cat(ss, 1).cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+# ---------------------------------------------------------------- permutation
+@pytest.mark.parametrize("T,H,E,k,pad,seed", [(300, 7168, 8, 2, 0, 1), (64, 256, 4, 1, 7, 2), (5, 128, 3, 3, 0, 3),
+                                              (40, 1024, 16, 0, 3, 4)])
+def test_permute_rows_and_fp8(oracle, dev, T, H, E, k, pad, seed):
+    """Expert-major permutation of MXFP4 rows (numpy indexing as the
+    reference) and the fused permutation + FP8 requant (oracle requant of the
+    permuted rows, zero padding rows included); also from payload-row views."""
+    from omo_python_api.permutation import mxfp4_permute, mxfp4_permute_to_fp8, payload_views
+    _say("permute", T, H, E, k, pad, seed)
+    rng = np.random.default_rng(seed)
+    q, s = scale_spread_payload(T, H // 2, seed, 16)
+    rm = np.zeros((T, E), bool)
+    for t in range(T):
+        rm[t, rng.choice(E, k, replace=False)] = True
+    probs = rng.random((T, E)).astype(np.float32)
+    e_idx, t_idx = np.nonzero(rm.T)  # expert-major, ascending tokens
+    n = t_idx.size
+    N = n + pad
+    exp_q = np.zeros((N, H // 2), np.uint8)
+    exp_s = np.zeros((N, H // 32), np.uint8)
+    exp_q[:n], exp_s[:n] = q[t_idx], s[t_idx]
+    exp_p = np.zeros(N, np.float32)
+    exp_p[:n] = probs[t_idx, e_idx]
+    qt, st = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
+    rmt = torch.from_numpy(rm).to(dev)
+    cq, cs, pp, src, msp = mxfp4_permute(qt, st, rmt, torch.from_numpy(probs).to(dev), N)
+    torch.cuda.synchronize()
+    assert msp == np.bincount(e_idx, minlength=E).tolist()
+    np.testing.assert_array_equal(src.cpu().numpy()[:n], t_idx)
+    assert (src.cpu().numpy()[n:] == -1).all()
+    np.testing.assert_array_equal(bits_u8(cq), exp_q)
+    np.testing.assert_array_equal(bits_u8(cs), exp_s)
+    np.testing.assert_array_equal(pp.cpu().numpy(), exp_p)
+    eo, es = oracle.mxfp4_to_fp8(exp_q, exp_s)
+    f8, f8s, _, _ = mxfp4_permute_to_fp8(qt, st, rmt, N, split=False)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits_u8(f8), eo)
+    np.testing.assert_array_equal(f8s.cpu().numpy().view(np.uint32), es.view(np.uint32))
+    # split the way omo_per_token_mxfp4ToFp8_wrapper does (padding rows as a trailing split)
+    f8l, f8sl, _, _ = mxfp4_permute_to_fp8(qt, st, rmt, N)
+    assert [t.shape[0] for t in f8l] == msp + ([pad] if pad else [])
+    np.testing.assert_array_equal(bits_u8(torch.cat(f8l)), eo)
+    # the same from payload rows [codes | scales], read in place through strided views
+    payload = torch.from_numpy(np.ascontiguousarray(np.concatenate([q, s], axis=1))).to(dev)
+    vq, vs = payload_views(payload)
+    cq2, cs2, _, _, _ = mxfp4_permute(vq, vs, rmt, None, N)
+    f82, f8s2, _, _ = mxfp4_permute_to_fp8(vq, vs, rmt, N, split=False)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits_u8(cq2), exp_q)
+    np.testing.assert_array_equal(bits_u8(cs2), exp_s)
+    np.testing.assert_array_equal(bits_u8(f82), eo)
+    np.testing.assert_array_equal(f8s2.cpu().numpy().view(np.uint32), es.view(np.uint32))
