@@ -137,6 +137,28 @@ OMO_API int omo_hip_quant_mxfp4_dual(const void* input, int64_t rows, int64_t co
                              void* row_s, int64_t row_s_bytes, void* col_q, int64_t col_q_bytes, void* col_s,
                              int64_t col_s_bytes, float eps, void* stream);
 
+/* One tensor of a grouped dual-layout quantize (host struct; pointers are
+ * device memory; sizes as in omo_hip_quant_mxfp4_dual). */
+typedef struct omo_dual_item {
+  const void* input;
+  int64_t rows, cols;
+  void* row_q;
+  int64_t row_q_bytes;
+  void* row_s;
+  int64_t row_s_bytes;
+  void* col_q;
+  int64_t col_q_bytes;
+  void* col_s;
+  int64_t col_s_bytes;
+} omo_dual_item;
+
+/* omo_hip_quant_mxfp4_dual over `count` tensors in one launch (per 32
+ * tensors), e.g. the gate/up/down weights of all local experts, which TE
+ * quantizes one GEMM at a time (code/transformer_engine-2.8.diff:1463-1466
+ * per tensor). Each item is validated like the single-tensor call; outputs
+ * are identical to `count` separate calls. `items` is host memory. */
+OMO_API int omo_hip_quant_mxfp4_dual_grouped(const omo_dual_item* items, int64_t count, float eps, void* stream);
+
 /* Expert-parallel payload rows (code/megatron-0.15.0rc7.diff:32-63): row t
  * of a [rows, 17*cols/32] uint8 tensor holds the row's MXFP4 codes (cols/2
  * bytes) followed by its E8M0 scales (cols/32 bytes), the layout Megatron

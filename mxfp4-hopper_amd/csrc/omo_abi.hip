@@ -5,6 +5,8 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
+#include <vector>
 
 #include "../../include/omo_mxfp4.h"
 #include "omo_internal.h"
@@ -102,6 +104,24 @@ int check_permute(const char* fn, const void* codes, int64_t codes_bytes, int64_
   REQUIRE_BUF("scales", scales, scales_bytes, scale_need);
   REQUIRE(num_out == 0 || src_rows != nullptr, "%s: src_rows: null pointer", fn);
   REQUIRE(aligned(src_rows, 4), "%s: src_rows must be 4-byte aligned", fn);
+  return OMO_OK;
+}
+
+// Checks of one dual-layout quantize (single or grouped).
+int check_dual(const char* fn, const void* input, int64_t rows, int64_t cols, const void* row_q, int64_t row_q_bytes,
+               const void* row_s, int64_t row_s_bytes, const void* col_q, int64_t col_q_bytes, const void* col_s,
+               int64_t col_s_bytes) {
+  REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", fn);
+  REQUIRE(rows % 32 == 0 && cols % 32 == 0, "%s: rows and cols must be multiples of 32 (got %lld x %lld)", fn,
+          (long long)rows, (long long)cols);
+  REQUIRE((rows / 32 + 1) * (cols / 256 + 1) < ((int64_t)1 << 30), "%s: too many tiles", fn);
+  const int64_t n = rows * cols;
+  REQUIRE_BUF("input", input, n, n);
+  REQUIRE_BUF("row_q", row_q, row_q_bytes, n / 2);
+  REQUIRE_BUF("row_s", row_s, row_s_bytes, n / 32);
+  REQUIRE_BUF("col_q", col_q, col_q_bytes, n / 2);
+  REQUIRE_BUF("col_s", col_s, col_s_bytes, n / 32);
+  REQUIRE(aligned(input, 16) && aligned(col_q, 16) && aligned(row_q, 4), "%s: misaligned buffer", fn);
   return OMO_OK;
 }
 
@@ -261,21 +281,39 @@ int omo_hip_quant_mxfp4_dual(const void* input, int64_t rows, int64_t cols, void
                              void* row_s, int64_t row_s_bytes, void* col_q, int64_t col_q_bytes, void* col_s,
                              int64_t col_s_bytes, float eps, void* stream) {
   const char* fn = "omo_quant_mxfp4_dual";
-  REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", fn);
-  REQUIRE(rows % 32 == 0 && cols % 32 == 0, "%s: rows and cols must be multiples of 32 (got %lld x %lld)", fn,
-          (long long)rows, (long long)cols);
-  REQUIRE((rows / 32 + 1) * (cols / 256 + 1) < ((int64_t)1 << 30), "%s: too many tiles", fn);
   REQUIRE(std::isfinite(eps), "%s: eps must be finite", fn);
-  const int64_t n = rows * cols;
-  REQUIRE_BUF("input", input, n, n);
-  REQUIRE_BUF("row_q", row_q, row_q_bytes, n / 2);
-  REQUIRE_BUF("row_s", row_s, row_s_bytes, n / 32);
-  REQUIRE_BUF("col_q", col_q, col_q_bytes, n / 2);
-  REQUIRE_BUF("col_s", col_s, col_s_bytes, n / 32);
-  REQUIRE(aligned(input, 16) && aligned(col_q, 16) && aligned(row_q, 4), "%s: misaligned buffer", fn);
-  if (n == 0) return ok();
+  int rc = check_dual(fn, input, rows, cols, row_q, row_q_bytes, row_s, row_s_bytes, col_q, col_q_bytes, col_s,
+                      col_s_bytes);
+  if (rc != OMO_OK) return rc;
+  if (rows == 0 || cols == 0) return ok();
   return from_hip(omo_hip::launch_quant_dual(input, row_q, row_s, col_q, col_s, rows, cols, eps, as_stream(stream)),
                   fn);
+}
+
+int omo_hip_quant_mxfp4_dual_grouped(const omo_dual_item* items, int64_t count, float eps, void* stream) {
+  const char* fn = "omo_quant_mxfp4_dual_grouped";
+  REQUIRE(count >= 0 && count <= ((int64_t)1 << 20), "%s: bad item count %lld", fn, (long long)count);
+  REQUIRE(count == 0 || items != nullptr, "%s: items: null pointer", fn);
+  REQUIRE(std::isfinite(eps), "%s: eps must be finite", fn);
+  std::vector<omo_hip::DualSpec> specs;
+  specs.reserve((size_t)count);
+  int64_t tiles = 0;
+  for (int64_t i = 0; i < count; i++) {
+    const omo_dual_item& it = items[i];
+    int rc = check_dual(fn, it.input, it.rows, it.cols, it.row_q, it.row_q_bytes, it.row_s, it.row_s_bytes, it.col_q,
+                        it.col_q_bytes, it.col_s, it.col_s_bytes);
+    if (rc != OMO_OK) {
+      char item_msg[64];
+      snprintf(item_msg, sizeof(item_msg), " (item %lld)", (long long)i);
+      strncat(g_err, item_msg, sizeof(g_err) - strlen(g_err) - 1);
+      return rc;
+    }
+    specs.push_back({it.input, it.row_q, it.row_s, it.col_q, it.col_s, it.rows, it.cols});
+    tiles += (it.rows / 32 + 1) * (it.cols / 256 + 1);
+  }
+  REQUIRE(tiles < ((int64_t)1 << 30), "%s: too many tiles", fn);
+  if (count == 0) return ok();
+  return from_hip(omo_hip::launch_quant_dual_grouped(specs.data(), (int)count, eps, as_stream(stream)), fn);
 }
 
 int omo_hip_quant_mxfp4_packed(const void* input, int64_t rows, int64_t cols, void* output, int64_t output_bytes,

@@ -50,4 +50,13 @@ hipError_t launch_gather_rows(const void* a, int64_t a_stride, int64_t a_bytes, 
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
                              float eps, hipStream_t stream);
 
+// One tensor of a grouped dual-layout quantize (validated by the ABI layer).
+struct DualSpec {
+  const void* x;
+  void *row_q, *row_s, *col_q, *col_s;
+  int64_t M, K;
+};
+
+hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps, hipStream_t stream);
+
 }  // namespace omo_hip

@@ -31,16 +31,14 @@ constexpr int kDualRows = 64;
 constexpr int kDualCols = 256;
 constexpr int kDualPitch = kDualCols * 2 + 16;  // bytes per LDS row
 constexpr int kXcds = 8;
+constexpr int kDualGroupMax = 32;
 
-__global__ __launch_bounds__(256) void quant_dual_kernel(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
-                                                         uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
-                                                         uint8_t* __restrict__ col_s, int64_t M, int64_t K,
-                                                         int tiles_m, int tiles, int per_xcd, float eps, int c_eps) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+// One 64 x 256 tile (index `logical`, M-fastest) of the [M, K] tensor x.
+__device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
+                                          uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
+                                          uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_m,
+                                          int logical, float eps, int c_eps, uint8_t* tile) {
   const int t = threadIdx.x;
-  const int b = blockIdx.x;
-  const int logical = (b % kXcds) * per_xcd + b / kXcds;
-  if (logical >= tiles) return;
   const int64_t mt = logical % tiles_m, kt = logical / tiles_m;
   const int64_t m0 = mt * kDualRows, k0 = kt * kDualCols;
   const int rows_valid = (int)(M - m0 < kDualRows ? M - m0 : kDualRows);  // 32 or 64
@@ -112,6 +110,49 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint16_t* __restr
   col_s[(kc + 1) * (M / 32) + so] = (uint8_t)byte_b;
 }
 
+__global__ __launch_bounds__(256) void quant_dual_kernel(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
+                                                         uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
+                                                         uint8_t* __restrict__ col_s, int64_t M, int64_t K,
+                                                         int tiles_m, int tiles, int per_xcd, float eps, int c_eps) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+  const int b = blockIdx.x;
+  const int logical = (b % kXcds) * per_xcd + b / kXcds;
+  if (logical >= tiles) return;
+  dual_tile(x, row_q, row_s, col_q, col_s, M, K, tiles_m, logical, eps, c_eps, tile);
+}
+
+// Grouped form: one launch over up to kDualGroupMax tensors (e.g. the weights
+// of all local experts), whose tiles are numbered item after item and then
+// spread over the XCDs like the tiles of one tensor. The descriptor table
+// travels by value in the kernel arguments.
+struct DualItem {
+  const uint16_t* x;
+  uint32_t* row_q;
+  uint8_t* row_s;
+  uint8_t* col_q;
+  uint8_t* col_s;
+  int64_t M, K;
+  int tiles_m, tile_begin;  // first logical tile of this item
+};
+
+struct DualGroup {
+  DualItem item[kDualGroupMax];
+  int count, tiles, per_xcd, c_eps;
+  float eps;
+};
+
+__global__ __launch_bounds__(256) void quant_dual_grouped_kernel(const DualGroup g) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+  const int b = blockIdx.x;
+  const int logical = (b % kXcds) * g.per_xcd + b / kXcds;
+  if (logical >= g.tiles) return;
+  int i = 0;
+  while (i + 1 < g.count && logical >= g.item[i + 1].tile_begin) i++;
+  const DualItem& it = g.item[i];
+  dual_tile(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, it.tiles_m, logical - it.tile_begin, g.eps,
+            g.c_eps, tile);
+}
+
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
                              float eps, hipStream_t stream) {
   if (M == 0 || K == 0) return hipSuccess;
@@ -124,6 +165,38 @@ hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_
                      static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, (int)tiles_m, (int)tiles,
                      (int)per_xcd, eps, host_c_eps(eps, 6.0f));
   return hipGetLastError();
+}
+
+hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps, hipStream_t stream) {
+  for (int base = 0; base < count; base += kDualGroupMax) {
+    DualGroup g;
+    memset(&g, 0, sizeof(g));
+    g.count = count - base < kDualGroupMax ? count - base : kDualGroupMax;
+    int tiles = 0;
+    for (int j = 0; j < g.count; j++) {
+      const DualSpec& d = items[base + j];
+      DualItem& it = g.item[j];
+      it.x = static_cast<const uint16_t*>(d.x);
+      it.row_q = static_cast<uint32_t*>(d.row_q);
+      it.row_s = static_cast<uint8_t*>(d.row_s);
+      it.col_q = static_cast<uint8_t*>(d.col_q);
+      it.col_s = static_cast<uint8_t*>(d.col_s);
+      it.M = d.M;
+      it.K = d.K;
+      it.tiles_m = (int)((d.M + kDualRows - 1) / kDualRows);
+      it.tile_begin = tiles;
+      tiles += (d.M == 0 || d.K == 0) ? 0 : it.tiles_m * (int)((d.K + kDualCols - 1) / kDualCols);
+    }
+    if (tiles == 0) continue;
+    g.tiles = tiles;
+    g.per_xcd = (tiles + kXcds - 1) / kXcds;
+    g.eps = eps;
+    g.c_eps = host_c_eps(eps, 6.0f);
+    hipLaunchKernelGGL(quant_dual_grouped_kernel, dim3((unsigned)(g.per_xcd * kXcds)), dim3(256), 0, stream, g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace omo_hip

@@ -434,7 +434,9 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
     const int sft = (int)((reinterpret_cast<uintptr_t>(out) + (uintptr_t)o) & 15u);
     uint8_t* a16 = out + o - sft;
 #pragma unroll
-    for (int j = qq; j <= 8; j += 8) {
+    for (int it = 0; it < 2; it++) {
+      const int j = qq + 8 * it;  // lane 0 also takes the ninth block
+      if (j > 8) break;
       const int lo = max(0, sft - 16 * j), hi = min(16, rows_valid + sft - 16 * j);
       if (lo >= hi) continue;
       // dest block j holds piece bytes [16 j - sft, 16 j - sft + 16)

@@ -37,6 +37,7 @@ __all__ = [
     "omo_per_token_Mxfp4ToFp8_col",
     "omo_per_token_Mxfp4ToFp8",
     "omo_quant_mxfp4_dual",
+    "omo_quant_mxfp4_dual_grouped",
     "omo_quant_mxfp4_packed",
     "omo_packed_Mxfp4ToBf16_dequant",
     "omo_packed_Mxfp4ToFp8",
@@ -263,6 +264,31 @@ def omo_quant_mxfp4_dual(input, row_q, row_s, col_q, col_s, eps=1e-10):
             input.data_ptr(), input.size(0), input.size(1), row_q.data_ptr(), row_q.numel(), row_s.data_ptr(),
             row_s.numel(), col_q.data_ptr(), col_q.numel(), col_s.data_ptr(), col_s.numel(), float(eps), stream))
 
+
+
+def omo_quant_mxfp4_dual_grouped(inputs, outputs, eps=1e-10):
+    """omo_quant_mxfp4_dual over a list of 2-D bf16 tensors in one launch (per
+    32 tensors). outputs[i] = (row_q, row_s, col_q, col_s) of inputs[i]."""
+    from ._abi import DualItem
+    if len(inputs) != len(outputs):
+        raise RuntimeError("inputs and outputs differ in length")
+    items = (DualItem * max(1, len(inputs)))()
+    for i, (x, outs) in enumerate(zip(inputs, outputs)):
+        row_q, row_s, col_q, col_s = outs
+        for t, n in ((x, "input"), (row_q, "row_q"), (row_s, "row_s"), (col_q, "col_q"), (col_s, "col_s")):
+            _check_input(t, n)
+        _same_device(inputs[0], x, row_q, row_s, col_q, col_s)
+        if x.dim() != 2:
+            raise RuntimeError(f"input {i} must be 2-D")
+        _check_dtype(x, torch.bfloat16, "input")
+        for t, n in ((row_q, "row_q"), (row_s, "row_s"), (col_q, "col_q"), (col_s, "col_s")):
+            _check_dtype(t, torch.uint8, n)
+        items[i] = DualItem(x.data_ptr(), x.size(0), x.size(1), row_q.data_ptr(), row_q.numel(), row_s.data_ptr(),
+                            row_s.numel(), col_q.data_ptr(), col_q.numel(), col_s.data_ptr(), col_s.numel())
+    if not inputs:
+        return
+    with _on_device(inputs[0]) as stream:
+        _check(_lib.omo_hip_quant_mxfp4_dual_grouped(items, len(inputs), float(eps), stream))
 
 # ---------------------------------------------------------------- payload rows
 # The expert-parallel payload row [codes (H/2 B) | E8M0 scales (H/32 B)] that

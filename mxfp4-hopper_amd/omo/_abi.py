@@ -17,6 +17,13 @@ OMO_ERR_HIP = -3
 
 _P, _I64, _I, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
+class DualItem(ctypes.Structure):
+    """omo_dual_item of include/omo_mxfp4.h."""
+    _fields_ = [("input", _P), ("rows", _I64), ("cols", _I64), ("row_q", _P), ("row_q_bytes", _I64),
+                ("row_s", _P), ("row_s_bytes", _I64), ("col_q", _P), ("col_q_bytes", _I64), ("col_s", _P),
+                ("col_s_bytes", _I64)]
+
+
 # name -> argtypes, in the order of include/omo_mxfp4.h
 SIGNATURES = {
     "omo_hip_per_token_group_quant_fp4": [_P, _I64, _P, _I64, _P, _I64, _I, _F, _F, _F, _I, _P],
@@ -29,6 +36,7 @@ SIGNATURES = {
     "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit": [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P,
                                                         _I64, _I64, _F, _P],
     "omo_hip_quant_mxfp4_dual": [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _F, _P],
+    "omo_hip_quant_mxfp4_dual_grouped": [ctypes.POINTER(DualItem), _I64, _F, _P],
     "omo_hip_quant_mxfp4_packed": [_P, _I64, _I64, _P, _I64, _F, _P],
     "omo_hip_packed_Mxfp4ToBf16_dequant": [_P, _I64, _I64, _P, _I64, _P],
     "omo_hip_packed_Mxfp4ToFp8": [_P, _I64, _I64, _P, _I64, _P, _I64, _P],

@@ -8,7 +8,7 @@ from typing import Optional
 
 import torch
 
-from omo import omo_per_token_group_quant_fp4, omo_quant_mxfp4_dual
+from omo import omo_per_token_group_quant_fp4, omo_quant_mxfp4_dual, omo_quant_mxfp4_dual_grouped
 
 fp8_type_ = torch.float8_e4m3fn
 uint8_type = torch.uint8
@@ -148,3 +148,22 @@ def omo_per_token_group_quant_mxfp4_dual(x: torch.Tensor, eps: float = 1e-10):
     if M > 0 and K > 0:
         omo_quant_mxfp4_dual(x, row_q, row_s, col_q, col_s, eps)
     return row_q, row_s, col_q, col_s
+
+
+def omo_per_token_group_quant_mxfp4_dual_grouped(xs, eps: float = 1e-10):
+    """omo_per_token_group_quant_mxfp4_dual over a list of 2-D bf16 tensors
+    (e.g. the gate/up/down weights of all local experts) in one launch; returns
+    one (row codes, row scales, col codes, col scales) tuple per tensor."""
+    outs = []
+    for x in xs:
+        assert x.dim() == 2, "every tensor must be 2-D"
+        M, K = x.shape
+        assert M % 32 == 0 and K % 32 == 0, "both dimensions must be multiples of 32"
+        assert x.is_contiguous(), "tensors must be contiguous"
+        outs.append((torch.empty((M, K // 2), device=x.device, dtype=uint8_type),
+                     torch.empty((M, K // 32), device=x.device, dtype=uint8_type),
+                     torch.empty((K, M // 2), device=x.device, dtype=uint8_type),
+                     torch.empty((K, M // 32), device=x.device, dtype=uint8_type)))
+    if xs:
+        omo_quant_mxfp4_dual_grouped(list(xs), outs, eps)
+    return outs

@@ -25,7 +25,7 @@ def test_header_declares_the_reference_entry_points():
               "omo_hip_per_token_Mxfp4ToFp8_col", "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col",
               "omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit", "omo_hip_quant_mxfp4_dual",
               "omo_hip_quant_mxfp4_packed", "omo_hip_packed_Mxfp4ToBf16_dequant", "omo_hip_packed_Mxfp4ToFp8",
-              "omo_hip_mxfp4_permute_rows", "omo_hip_permute_Mxfp4ToFp8",
+              "omo_hip_mxfp4_permute_rows", "omo_hip_permute_Mxfp4ToFp8", "omo_hip_quant_mxfp4_dual_grouped",
               "omo_hip_abi_version", "omo_hip_status_string", "omo_hip_last_error"]:
         assert n in names
 
@@ -203,3 +203,17 @@ def test_permute_validation_paths():
     # nothing to do
     assert lib.omo_hip_permute_Mxfp4ToFp8(f, 1 << 20, 64, f, 1 << 20, 4, 4, 128, None, 0, None, 0, None, 0,
                                           None) == 0
+
+
+def test_dual_grouped_validation_paths():
+    from omo._abi import DualItem
+    lib = _lib()
+    f = 0x1000
+    good = DualItem(f, 32, 32, f, 512, f, 32, f, 512, f, 32)
+    bad = DualItem(f, 48, 32, f, 768, f, 48, f, 768, f, 48)  # rows % 32
+    arr = (DualItem * 2)(good, bad)
+    assert lib.omo_hip_quant_mxfp4_dual_grouped(arr, 2, 1e-10, None) == -1
+    assert b"item 1" in lib.omo_hip_last_error()
+    assert lib.omo_hip_quant_mxfp4_dual_grouped(arr, 1, float("nan"), None) == -1
+    assert lib.omo_hip_quant_mxfp4_dual_grouped(None, 3, 1e-10, None) == -1
+    assert lib.omo_hip_quant_mxfp4_dual_grouped(None, 0, 1e-10, None) == 0

@@ -438,6 +438,28 @@ def test_dual_layout(oracle, dev, M, K, seed):
     np.testing.assert_array_equal(bits_u8(cs).reshape(-1), est)
 
 
+def test_dual_layout_grouped(oracle, dev):
+    """One grouped launch over tensors of different shapes (more than one
+    32-tensor launch, an empty tensor among them) == the oracle per tensor."""
+    from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4_dual_grouped
+    shapes = [(64, 256), (96, 1056), (0, 64), (32, 32), (256, 2048)] * 7  # 35 tensors
+    _say("dual grouped", len(shapes))
+    g = torch.Generator().manual_seed(9)
+    xs = [(torch.randn(sh, generator=g) * (1 + i)).to(torch.bfloat16) for i, sh in enumerate(shapes)]
+    outs = omo_per_token_group_quant_mxfp4_dual_grouped([x.to(dev) for x in xs])
+    torch.cuda.synchronize()
+    for x, (rq, rs, cq, cs) in zip(xs, outs):
+        if x.numel() == 0:
+            continue
+        xb = bits_u16(x)
+        eq, es = oracle.quant_mxfp4(xb.reshape(-1))
+        np.testing.assert_array_equal(bits_u8(rq).reshape(-1), eq)
+        np.testing.assert_array_equal(bits_u8(rs).reshape(-1), es)
+        eqt, est = oracle.quant_mxfp4(np.ascontiguousarray(xb.T).reshape(-1))
+        np.testing.assert_array_equal(bits_u8(cq).reshape(-1), eqt)
+        np.testing.assert_array_equal(bits_u8(cs).reshape(-1), est)
+
+
 # ------------------------------------------------- expert-parallel payload rows
 def _payload(codes, scales):
     """Megatron's torch.cat of codes [T, H/2] and scales [T, H/32] (numpy)."""
