@@ -389,10 +389,10 @@ struct MsplitSmem {
 // A split's output column c is a run of len bytes at off*N + c*len, so the
 // tile's 128-row piece of a column starts at an arbitrary byte alignment.
 // The tile's output columns are staged in LDS; lane q of a column then
-// writes the q-th 16 B aligned block of the column's piece (lane 0 also the
-// ninth), taking the bytes from LDS with v_alignbyte_b32 over five dwords.
-// Full blocks are single 16 B stores; only the first and last block of a
-// piece are written in smaller pieces.
+// writes the q-th 16 B aligned block of the column's piece, taking the bytes
+// from LDS with v_alignbyte_b32 over five dwords. Full blocks are single 16 B
+// stores; only the first and last (ninth) block of a piece are written in
+// smaller pieces, for both columns of an octet in the same pass.
 __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
@@ -425,35 +425,54 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
   }
   *reinterpret_cast<u32x4*>(&sm.obuf[2 * p][16 + 16 * qq]) = res.e0;
   *reinterpret_cast<u32x4*>(&sm.obuf[2 * p + 1][16 + 16 * qq]) = res.e1;
-  __syncthreads();
+  // The 8 lanes of a column are in one wave and read only columns their
+  // wave wrote: a wave-level fence orders the LDS writes before the reads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (col0 + 2 * p >= N) return;  // N is even: both columns or neither
+  // Three passes: blocks 1..7 of column 2p, then of column 2p + 1 (lanes
+  // 1..7, whole unless the piece is short), then the four usually partial
+  // end blocks side by side: block 0 of column 2p (lane 0) and of 2p + 1
+  // (lane 1), block 8 of 2p (lane 7) and of 2p + 1 (lane 6).
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
+  for (int pass = 0; pass < 3; pass++) {
+    int h, j;
+    if (pass < 2) {
+      if (qq == 0) continue;
+      h = pass;
+      j = qq;
+    } else {
+      if (qq == 0 || qq == 1) {
+        h = qq;
+        j = 0;
+      } else if (qq == 7 || qq == 6) {
+        h = 7 - qq;
+        j = 8;
+      } else {
+        continue;
+      }
+    }
     const int c = 2 * p + h;
     const int64_t o = start * N + (col0 + c) * len + bm * kTile;  // this tile's piece of column c
     const int sft = (int)((reinterpret_cast<uintptr_t>(out) + (uintptr_t)o) & 15u);
     uint8_t* a16 = out + o - sft;
-#pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int j = qq + 8 * it;  // lane 0 also takes the ninth block
-      if (j > 8) break;
-      const int lo = max(0, sft - 16 * j), hi = min(16, rows_valid + sft - 16 * j);
-      if (lo >= hi) continue;
-      // dest block j holds piece bytes [16 j - sft, 16 j - sft + 16)
-      const int b = 16 + 16 * j - sft;
-      const uint32_t* dw = reinterpret_cast<const uint32_t*>(&sm.obuf[c][b & ~3]);
-      const uint32_t sh = (uint32_t)(b & 3);
-      const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2], d3 = dw[3], d4 = dw[4];
-      u32x4 blk;
-      blk[0] = __builtin_amdgcn_alignbyte(d1, d0, sh);
-      blk[1] = __builtin_amdgcn_alignbyte(d2, d1, sh);
-      blk[2] = __builtin_amdgcn_alignbyte(d3, d2, sh);
-      blk[3] = __builtin_amdgcn_alignbyte(d4, d3, sh);
-      if (lo == 0 && hi == 16) {
-        *reinterpret_cast<u32x4*>(a16 + 16 * j) = blk;
-      } else {
-        store_partial16(a16 + 16 * j, blk, lo, hi);
-      }
+    const int lo = max(0, sft - 16 * j), hi = min(16, rows_valid + sft - 16 * j);
+    if (lo >= hi) continue;
+    // dest block j holds piece bytes [16 j - sft, 16 j - sft + 16)
+    const int b = 16 + 16 * j - sft;
+    const uint32_t* dw = reinterpret_cast<const uint32_t*>(&sm.obuf[c][b & ~3]);
+    const uint32_t sh = (uint32_t)(b & 3);
+    const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2], d3 = dw[3], d4 = dw[4];
+    u32x4 blk;
+    blk[0] = __builtin_amdgcn_alignbyte(d1, d0, sh);
+    blk[1] = __builtin_amdgcn_alignbyte(d2, d1, sh);
+    blk[2] = __builtin_amdgcn_alignbyte(d3, d2, sh);
+    blk[3] = __builtin_amdgcn_alignbyte(d4, d3, sh);
+    if (lo == 0 && hi == 16) {
+      *reinterpret_cast<u32x4*>(a16 + 16 * j) = blk;
+    } else {
+      store_partial16(a16 + 16 * j, blk, lo, hi);
     }
   }
 }

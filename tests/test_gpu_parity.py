@@ -419,6 +419,28 @@ def test_row_to_fp8_col_msplit(oracle, dev, splits, N):
         soff += nb
 
 
+@pytest.mark.parametrize("splits,N", [([211, 97, 300, 5, 256, 130], 7168), ([2083, 17, 1965], 1024),
+                                      ([129, 255, 383, 1, 16, 144], 384)])
+def test_row_to_fp8_col_msplit_every_byte(oracle, dev, splits, N):
+    """Ragged splits (column runs at every byte alignment, pieces that end
+    inside a 16 B block) into outputs pre-filled with a sentinel, so a byte
+    the kernel fails to write cannot pass by holding an earlier result."""
+    import omo
+    from omo_python_api.mxfp4_dequant import split_metadata
+    _say("msplit every byte", splits, N)
+    M = sum(splits)
+    q, s = payload_from_normal(M, N, M % 89)
+    lens, offs, soffs, max_len, rows, srows = split_metadata(splits, dev)
+    out_q = torch.full((M * N,), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    out_s = torch.full((srows, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out_q,
+                                                    out_s, lens, offs, soffs, max_len, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(bits_u8(out_q), eo)
+    np.testing.assert_array_equal(out_s.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
 # ------------------------------------------------------------- dual layout
 @pytest.mark.parametrize("M,K,seed", [(32, 32, 1), (64, 7168, 2), (96, 1056, 3), (256, 256, 4)])
 def test_dual_layout(oracle, dev, M, K, seed):
