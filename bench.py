@@ -13,7 +13,9 @@ MoE-payload requant/dequant (4096 x 7168, both FP8 layouts), the fused
 expert-parallel payload rows against Megatron's cat/split composition, the
 cfg5 MoE layer composite (all codec launches of one layer on 8 local experts),
 the dual-layout quantize (7168 x 18432) and the row -> col FP8 conversion,
-each as GB/s of algorithmic bytes or microseconds per call.
+each as GB/s of algorithmic bytes or microseconds per call, and memory-only
+kernels over the headline buffers (the quantize's loads and stores without
+its arithmetic; streaming reads; streaming writes) as the practical bound.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        [--only quant|dequant|...] [--copy-calibration]
@@ -39,7 +41,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (>= 3 to exceed the 256 MB cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of legs: quant,dequant,payload,ep_payload,moe,dual,rowcol")
+    ap.add_argument("--only", default="",
+                    help="comma list of legs: quant,dequant,payload,ep_payload,moe,dual,rowcol,ceiling")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (known traffic) for counter calibration")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -410,6 +413,33 @@ def main():
         out["row_to_col_fp8"] = {"workload": "MXFP4 rowwise -> FP8 columnwise 4096x7168",
                                  "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
                                  "us_per_launch": round(t / steps * 1e3, 2)}
+
+    if want("ceiling"):
+        # memory-only kernels at the headline size: the quantize's loads and
+        # stores without its arithmetic, and pure streaming reads / writes
+        import ctypes
+        cl = ctypes.CDLL(os.path.join(ROOT, "mxfp4-hopper_amd", "lib", "libomo_ceiling.so"))
+        cl.omo_ceiling_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_int64, ctypes.c_void_p]
+        n16 = numel * 2 // 16
+        wbuf = [torch.empty(n16 * 16, dtype=torch.uint8, device=dev) for _ in range(args.sets)]
+        res = {}
+        for kind, name, nbytes in ((0, "quant_traffic", qbytes), (1, "read_stream", n16 * 16),
+                                   (2, "write_stream", n16 * 16)):
+            def mem(i, kind=kind):
+                dst = wbuf[i] if kind == 2 else qs[i]
+                rc = cl.omo_ceiling_launch(kind, xs[i].data_ptr(), dst.data_ptr(), ss[i].data_ptr(), n16, cur())
+                if rc:
+                    raise RuntimeError(f"omo_ceiling_launch({kind}) returned {rc}")
+            steps = max(100, args.steps // 2)
+            t, _ = time_launches(torch, mem, args.sets, steps, 20)
+            res[name] = (round(nbytes / (t / steps * 1e-3) / 1e9, 1), round(t / steps * 1e3, 3))
+        out["memory_ceiling"] = {
+            "workload": "memory-only kernels over the 8192x7168 headline buffers (mxfp4-hopper_amd/ceiling)",
+            "quant_traffic_GB/s": res["quant_traffic"][0], "quant_traffic_us": res["quant_traffic"][1],
+            "quant_frac_of_ceiling": round(value / res["quant_traffic"][0], 4),
+            "read_stream_GB/s": res["read_stream"][0], "write_stream_GB/s": res["write_stream"][0]}
+        del wbuf
 
     line = {
         "metric": METRIC,

@@ -1,0 +1,71 @@
+// Memory-only kernels that bound what the codec kernels can reach on this
+// HBM: the quantize's exact access pattern with its arithmetic removed, plus
+// pure streaming reads and writes. Built into a separate library used only
+// by bench.py; nothing in the product calls it.
+//
+// quant_traffic: lane t of workgroup b reads 16 B chunks c = 512 b + 256 k + t
+// (k = 0, 1) with non-temporal loads, writes one 4 B dword per chunk to
+// codes[c] (non-temporal) and, on every fourth lane, one byte to
+// scales[c / 4] - the loads and stores of the rowwise quantize kernel at two
+// chunks per lane.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void quant_traffic(const u32x4* __restrict__ in, uint32_t* __restrict__ codes,
+                                                     uint8_t* __restrict__ scales) {
+  const int64_t c0 = (int64_t)blockIdx.x * 512 + threadIdx.x;
+  u32x4 d[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) d[k] = __builtin_nontemporal_load(in + c0 + 256 * k);
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int64_t c = c0 + 256 * k;
+    const uint32_t v = d[k].x ^ d[k].y ^ d[k].z ^ d[k].w;
+    __builtin_nontemporal_store(v, codes + c);
+    if ((threadIdx.x & 3) == 0) scales[c >> 2] = (uint8_t)v;
+  }
+}
+
+__global__ __launch_bounds__(256) void read_stream(const u32x4* __restrict__ in, uint32_t* __restrict__ sink) {
+  const int64_t c0 = (int64_t)blockIdx.x * 512 + threadIdx.x;
+  const u32x4 a = __builtin_nontemporal_load(in + c0), b = __builtin_nontemporal_load(in + c0 + 256);
+  const uint32_t v = a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
+  if (v == 0x9E3779B9u) sink[blockIdx.x] = v;  // keeps the loads; data never matches in practice
+}
+
+__global__ __launch_bounds__(256) void write_stream(u32x4* __restrict__ out) {
+  const int64_t c0 = (int64_t)blockIdx.x * 512 + threadIdx.x;
+  const u32x4 v = {threadIdx.x, blockIdx.x, 0u, 1u};
+  __builtin_nontemporal_store(v, out + c0);
+  __builtin_nontemporal_store(v, out + c0 + 256);
+}
+
+// kind 0: quant_traffic over n16 input chunks (codes: 4 n16 B, scales: n16/4 B)
+// kind 1: read_stream over n16 chunks (sink: n16/512 dwords)
+// kind 2: write_stream of n16 chunks into `out`
+// n16 must be a positive multiple of 512. Returns a hipError_t value, or -1
+// for a bad size or kind.
+extern "C" __attribute__((visibility("default"))) int omo_ceiling_launch(int kind, const void* in, void* out,
+                                                                          void* out2, int64_t n16,
+                                                                          hipStream_t stream) {
+  if (n16 <= 0 || n16 % 512 != 0) return -1;
+  const dim3 grid((unsigned)(n16 / 512)), block(256);
+  switch (kind) {
+    case 0:
+      hipLaunchKernelGGL(quant_traffic, grid, block, 0, stream, static_cast<const u32x4*>(in),
+                         static_cast<uint32_t*>(out), static_cast<uint8_t*>(out2));
+      break;
+    case 1:
+      hipLaunchKernelGGL(read_stream, grid, block, 0, stream, static_cast<const u32x4*>(in),
+                         static_cast<uint32_t*>(out));
+      break;
+    case 2:
+      hipLaunchKernelGGL(write_stream, grid, block, 0, stream, static_cast<u32x4*>(out));
+      break;
+    default:
+      return -1;
+  }
+  return (int)hipGetLastError();
+}
