@@ -20,6 +20,15 @@ __device__ __forceinline__ uint32_t ref_scale(float amax, float fp4_max, float* 
   return (uint32_t)(c + 127) & 0xFFu;
 }
 
+// fmaxf(m, |x|) for the bf16 pattern x, skipping every NaN pattern. The
+// reference's CUDA fmaxf drops NaN operands, signalling ones included; the
+// hardware max in IEEE mode returns a quiet NaN for a signalling operand,
+// which would restart a running maximum after an sNaN input.
+__device__ __forceinline__ float fmax_abs_bf16(float m, uint32_t x) {
+  const uint32_t a = x & 0x7FFFu;
+  return a <= 0x7F80u ? fmaxf(m, bf16_to_f32(a)) : m;
+}
+
 // Emulation of the reference for one chunk of a quad. All four lanes of the
 // quad must call it together (DPP reduction).
 __device__ __forceinline__ void quant_chunk_ref(const u32x4& d, float eps, float fp4_min, float fp4_max,
@@ -28,8 +37,8 @@ __device__ __forceinline__ void quant_chunk_ref(const u32x4& d, float eps, float
   float amax = eps;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    amax = fmaxf(amax, fabsf(bf16_to_f32(w[k] & 0xFFFFu)));
-    amax = fmaxf(amax, fabsf(bf16_to_f32(w[k] >> 16)));
+    amax = fmax_abs_bf16(amax, w[k]);
+    amax = fmax_abs_bf16(amax, w[k] >> 16);
   }
   amax = quad_fmax(amax);
   float inv;
@@ -96,8 +105,8 @@ __device__ __forceinline__ u32x4 quant_block32_ref(const uint32_t (&p)[16], floa
   float amax = eps;
 #pragma unroll
   for (int k = 0; k < 16; k++) {
-    amax = fmaxf(amax, fabsf(bf16_to_f32(p[k] & 0xFFFFu)));
-    amax = fmaxf(amax, fabsf(bf16_to_f32(p[k] >> 16)));
+    amax = fmax_abs_bf16(amax, p[k]);
+    amax = fmax_abs_bf16(amax, p[k] >> 16);
   }
   float inv;
   *byte = ref_scale(amax, fp4_max, &inv);

@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(QuantArgs a) {
     uint32_t codes, byte;
     if (STANDARD) {
       uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
-      if (am < 0x7F80u) {
+      if (__builtin_expect(am < 0x7F80u, 1)) {
         codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
       } else {
         quant_chunk_ref(d[u], a.eps, a.fp4_min, a.fp4_max, &codes, &byte);
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantRowsArgs a) {
     if (c >= cpr) continue;  // whole quads
     uint32_t codes, byte;
     const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
-    if (am < 0x7F80u) {
+    if (__builtin_expect(am < 0x7F80u, 1)) {
       codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
     } else {
       quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);

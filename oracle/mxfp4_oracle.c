@@ -197,9 +197,15 @@ static void quant_range(void* p, int64_t g0, int64_t g1) {
   const quant_ctx* c = (const quant_ctx*)p;
   for (int64_t g = g0; g < g1; g++) {
     const uint16_t* in = c->x + g * 32;
-    /* amax over the 32 elements, seeded with eps; fmaxf drops NaN (:151,170-178) */
+    /* amax over the 32 elements, seeded with eps; the reference's fmaxf drops
+       every NaN, signalling ones included (:151,170-178). glibc's fmaxf returns
+       a quiet NaN when an operand is signalling, which would restart the
+       maximum after an sNaN, so the NaN test is a comparison here. */
     float amax = c->eps;
-    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(bf16_to_f32(in[j])));
+    for (int j = 0; j < 32; j++) {
+      const float a = fabsf(bf16_to_f32(in[j]));
+      if (a > amax) amax = a;
+    }
     float y_s;
     c->s[g] = scale_rule(amax, c->fmax, &y_s);
     const float inv_y_s = 1.0f / y_s; /* :200 */

@@ -240,6 +240,14 @@ def main():
         anchor = bf16_bits_of(6.0 * 2.0 ** e) if e < 127 else 0x7F7F
         blocks.append([anchor] + [bf16_bits_of((k + 1) * 6.0 * 2.0 ** e / 33.0) ^ (0x8000 if k % 3 == 0 else 0)
                                   for k in range(31)])
+    # NaNs after the block maximum, signalling ones included, within one
+    # 8-element group: every NaN is ignored by the amax
+    blocks += [
+        [0x40C8, 0x7F81] + [0x3F80] * 30,
+        [0x3F80] * 5 + [0xC0C8, 0xFF81, 0x3F00] + [0x3F80] * 24,
+        [0x40C8, 0x7FC0, 0x7F81, 0xFFC0] + [0x3F00] * 28,
+        [0x3F00] * 31 + [0x7F81],
+    ]
     quant = []
     for b in blocks:
         sc, codes = quantize_block(b)

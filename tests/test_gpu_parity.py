@@ -65,6 +65,9 @@ def special_blocks():
         [0x40C0] + [0x3E80, 0x3F40, 0x3FA0, 0x3FE0, 0x4020, 0x4060, 0x40A0, 0x40B0] * 3 + [0] * 7,
         [0x2F00] * 32,                               # below eps*6: eps dominates
         [0x3040] + [0x2FFF] * 31,                    # 6*2^-33 anchor
+        [0x40C8, snan] + [one] * 30,                 # sNaN after the max, same 8-element group
+        [one] * 5 + [0xC0C8, 0xFF81, half] + [one] * 24,
+        [0x40C8, qnan, snan, nqnan] + [half] * 28,
     ]
     return np.array(rows, dtype=np.uint16).reshape(-1)
 
@@ -460,6 +463,38 @@ def test_dual_layout(oracle, dev, M, K, seed):
     np.testing.assert_array_equal(bits_u8(cs).reshape(-1), est)
 
 
+@pytest.mark.parametrize("M,K,seed", [(96, 1056, 5), (192, 7168, 6), (64, 32, 7)])
+def test_dual_layout_every_byte_special_columns(oracle, dev, M, K, seed):
+    """Special-value blocks placed down columns (inside the second 16-row half
+    of a 32-row block, and across two blocks), outputs pre-filled with a
+    sentinel so every byte must be written."""
+    import omo
+    _say("dual every byte", M, K)
+    x = (torch.randn((M, K), generator=torch.Generator().manual_seed(seed)) * 3).to(torch.bfloat16)
+    xb = bits_u16(x)
+    sb = special_blocks()
+    nblk = sb.size // 32
+    for i, c in enumerate(range(1, K, 7)):
+        blk = sb[32 * (i % nblk): 32 * (i % nblk + 1)]
+        if i % 3 == 0:
+            xb[16:32, c] = blk[:16]  # half 1 of block 0 only
+        elif M >= 64:
+            xb[16:48, c] = blk  # straddles blocks 0 and 1
+        else:
+            xb[0:32, c] = blk
+    xd = from_u16(xb, dev)
+    fill = lambda *shape: torch.full(shape, 0xAB, dtype=torch.uint8, device=dev)  # noqa: E731
+    rq, rs, cq, cs = fill(M, K // 2), fill(M, K // 32), fill(K, M // 2), fill(K, M // 32)
+    omo.omo_quant_mxfp4_dual(xd, rq, rs, cq, cs, 1e-10)
+    torch.cuda.synchronize()
+    eq, es = oracle.quant_mxfp4(xb.reshape(-1))
+    np.testing.assert_array_equal(bits_u8(rq).reshape(-1), eq)
+    np.testing.assert_array_equal(bits_u8(rs).reshape(-1), es)
+    eqt, est = oracle.quant_mxfp4(np.ascontiguousarray(xb.T).reshape(-1))
+    np.testing.assert_array_equal(bits_u8(cq).reshape(-1), eqt)
+    np.testing.assert_array_equal(bits_u8(cs).reshape(-1), est)
+
+
 def test_dual_layout_grouped(oracle, dev):
     """One grouped launch over tensors of different shapes (more than one
     32-tensor launch, an empty tensor among them) == the oracle per tensor."""
@@ -489,7 +524,7 @@ def _payload(codes, scales):
     return np.ascontiguousarray(np.concatenate([codes.reshape(T, -1), scales.reshape(T, -1)], axis=1))
 
 
-@pytest.mark.parametrize("T,H,seed", [(1, 128, 1), (300, 7168, 2), (64, 2048, 3), (4, 128, 0), (0, 7168, 5)])
+@pytest.mark.parametrize("T,H,seed", [(1, 128, 1), (300, 7168, 2), (64, 2048, 3), (5, 128, 0), (0, 7168, 5)])
 def test_payload_quant(oracle, dev, T, H, seed):
     """Quantize into payload rows == torch.cat of the unfused quantize outputs."""
     from omo_python_api.ep_payload import fp4_quantize_packed, pack_rowwise_components
