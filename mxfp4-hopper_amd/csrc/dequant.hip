@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __res
   for (int u = 0; u < UNROLL; u++) {
     const int64_t i = base + (int64_t)u * 256;
     if (i < ndw) {
-      c[u] = __builtin_nontemporal_load(q + i);
+      c[u] = q[i];
       sb[u] = s[i >> 2];
     }
   }
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
   for (int u = 0; u < UNROLL; u++) {
     const int i = base + u * 256;
     if (i < dpr) {
-      c[u] = __builtin_nontemporal_load(qr + i);
+      c[u] = qr[i];
       sb[u] = sr[i >> 2];
     }
   }

@@ -24,6 +24,10 @@
 // hold a full tile column: the column amax is two quad_perm steps and one
 // row_half_mirror step of DPP, and the eight lanes write the column's 128
 // output rows as eight contiguous 16 B pieces.
+// Code loads are ordinary (temporal) loads: a tile reads one 64 B half of
+// each 128 B code line and the next column tile the other half, which then
+// usually hits in L2; with non-temporal loads the dense kernel took 16.6 us
+// instead of 12.7 us at 4096 x 7168.
 // When all 16 scale bytes of a lane lie in [1, 252] no product can be inf
 // or NaN, and v_cvt_scalef32_pk_f32_fp4 gives both columns' exact fp32
 // values of a row in one instruction; otherwise the lane restates the
@@ -82,7 +86,7 @@ __device__ __forceinline__ StageRegs rc_load(const uint8_t* __restrict__ q, cons
     if (r < rows_valid && gcol < N) {
       const uint8_t* src = q + (row0 + r) * half + gcol / 2;
       if (vin && gcol + 32 <= N) {
-        w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+        w = *reinterpret_cast<const u32x4*>(src);
       } else {
         const int nb = (int)((N - gcol) / 2 < 16 ? (N - gcol) / 2 : 16);
         for (int j = 0; j < nb; j++) w[j >> 2] |= (uint32_t)src[j] << (8 * (j & 3));
@@ -115,8 +119,7 @@ __device__ __forceinline__ StageRegs rc_load_full(const uint8_t* __restrict__ q,
                                                   int64_t N, int64_t row0, int64_t col0) {
   const int t = threadIdx.x;
   StageRegs g;
-  g.codes = __builtin_nontemporal_load(
-      reinterpret_cast<const u32x4*>(q + (row0 + (t >> 2)) * (N / 2) + col0 / 2 + (t & 3) * 16));
+  g.codes = *reinterpret_cast<const u32x4*>(q + (row0 + (t >> 2)) * (N / 2) + col0 / 2 + (t & 3) * 16);
   g.scales = *reinterpret_cast<const uint32_t*>(s + (row0 + (t & (kTile - 1))) * (N / 32) + col0 / 32);
   return g;
 }
