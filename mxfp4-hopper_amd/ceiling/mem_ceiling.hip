@@ -42,9 +42,45 @@ __global__ __launch_bounds__(256) void write_stream(u32x4* __restrict__ out) {
   __builtin_nontemporal_store(v, out + c0 + 256);
 }
 
+// two_phase_traffic: the same loads and stores in the two-phase schedule of
+// quant_phased_kernel: one 1024-thread workgroup per CU reads its whole
+// share (keeping 4 B per chunk and a byte per 4 chunks in LDS), then writes
+// it out as 16 B stores.
+__global__ __launch_bounds__(1024) void two_phase_traffic(const u32x4* __restrict__ in, uint32_t* __restrict__ codes,
+                                                          uint8_t* __restrict__ scales, int share) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t tp_lds[];
+  uint8_t* lsc = reinterpret_cast<uint8_t*>(tp_lds + share);
+  const int64_t base = (int64_t)blockIdx.x * share;
+  for (int i0 = 0; i0 < share; i0 += 2048) {
+    u32x4 d[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int i = i0 + u * 1024 + (int)threadIdx.x;
+      d[u] = i < share ? __builtin_nontemporal_load(in + base + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int i = i0 + u * 1024 + (int)threadIdx.x;
+      if (i < share) {
+        const uint32_t v = d[u].x ^ d[u].y ^ d[u].z ^ d[u].w;
+        tp_lds[i] = v;
+        if ((i & 3) == 0) lsc[i >> 2] = (uint8_t)v;
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = (int)threadIdx.x * 4; i < share; i += 4096)
+    __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&tp_lds[i]), reinterpret_cast<u32x4*>(codes + base + i));
+  for (int i = (int)threadIdx.x * 16; i < share / 4; i += 16384)
+    *reinterpret_cast<u32x4*>(scales + base / 4 + i) = *reinterpret_cast<const u32x4*>(lsc + i);
+}
+
 // kind 0: quant_traffic over n16 input chunks (codes: 4 n16 B, scales: n16/4 B)
 // kind 1: read_stream over n16 chunks (sink: n16/512 dwords)
 // kind 2: write_stream of n16 chunks into `out`
+// kind 3: two_phase_traffic over n16 chunks (as kind 0), one workgroup per CU;
+//         needs n16 to be a multiple of 64 x the CU count and the share to
+//         fit the LDS of one workgroup
 // n16 must be a positive multiple of 512. Returns a hipError_t value, or -1
 // for a bad size or kind.
 extern "C" __attribute__((visibility("default"))) int omo_ceiling_launch(int kind, const void* in, void* out,
@@ -64,6 +100,20 @@ extern "C" __attribute__((visibility("default"))) int omo_ceiling_launch(int kin
     case 2:
       hipLaunchKernelGGL(write_stream, grid, block, 0, stream, static_cast<u32x4*>(out));
       break;
+    case 3: {
+      int dev = 0, cus = 0, lds = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+          hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || cus <= 0)
+        return -1;
+      if (n16 % ((int64_t)cus * 64) != 0) return -1;
+      const int share = (int)(n16 / cus);
+      const size_t bytes = (size_t)share * 4 + share / 4;
+      if (bytes > (size_t)lds) return -1;
+      hipLaunchKernelGGL(two_phase_traffic, dim3((unsigned)cus), dim3(1024), bytes, stream,
+                         static_cast<const u32x4*>(in), static_cast<uint32_t*>(out), static_cast<uint8_t*>(out2), share);
+      break;
+    }
     default:
       return -1;
   }

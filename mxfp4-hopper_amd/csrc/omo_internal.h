@@ -59,4 +59,12 @@ struct DualSpec {
 
 hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps, hipStream_t stream);
 
+// Properties of the current device, queried once per device and cached:
+// compute units, and the largest LDS allocation of one workgroup in bytes.
+struct DeviceCaps {
+  int cus;
+  int lds_per_workgroup;
+};
+DeviceCaps current_device_caps();
+
 }  // namespace omo_hip

@@ -150,6 +150,41 @@ def test_quant_cfg2_north_star(oracle, dev):
     np.testing.assert_array_equal(q, eq)
 
 
+@pytest.mark.parametrize("case", ["domain_tiled", "partial_last_workgroup", "steps_below_95"])
+def test_quant_two_phase_path(oracle, dev, case):
+    """Shapes around the two-phase kernel (one LDS round per CU, then 16 B
+    stores; taken when a CU's share is one round of at least 4096 chunks
+    that fills its 2048-chunk steps to 95%). On a 256-CU device:
+    every bf16 value under every scale exponent plus the special blocks in
+    exactly 2 steps per CU; a share of 7 steps whose last workgroup ends
+    early with a scale-byte tail that is not a multiple of 16; and a share
+    of 8.03 steps, which takes the one-pass kernel. Outputs start as a
+    sentinel, so every byte must be written."""
+    _say("quant two-phase", case)
+    if case == "domain_tiled":
+        dom, _ = domain_blocks()
+        unit = np.concatenate([dom, special_blocks()])
+        xb = np.tile(unit, -(-(1 << 23) // unit.size))[: 1 << 23]
+        shape = (xb.size // 2048, 2048)
+    elif case == "partial_last_workgroup":
+        shape = (5, 5865632)  # 3,666,020 chunks: 255 shares of 14,336 and one of 10,340
+        g = torch.Generator().manual_seed(32)
+        xb = bits_u16((torch.randn(shape, generator=g) * 1e-3).to(torch.bfloat16)).reshape(-1)
+    else:
+        shape = (16431, 2048)
+        g = torch.Generator().manual_seed(31)
+        xb = bits_u16((torch.randn(shape, generator=g) * 5).to(torch.bfloat16)).reshape(-1)
+    omo = _omo()
+    x = from_u16(xb, dev).view(shape)
+    q = torch.full((xb.size // 2,), 0xAB, dtype=torch.uint8, device=dev)
+    s = torch.full((shape[0], xb.size // 32 // shape[0]), 0xAB, dtype=torch.uint8, device=dev)
+    omo.omo_per_token_group_quant_fp4(x, q, s, 32, 1e-10, -6.0, 6.0, False)
+    torch.cuda.synchronize()
+    eq, es = oracle.quant_mxfp4(xb)
+    np.testing.assert_array_equal(bits_u8(s).reshape(-1), es)
+    np.testing.assert_array_equal(bits_u8(q), eq)
+
+
 def test_quant_wrapper_and_determinism(oracle, dev):
     from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
     _say("quant wrapper")
