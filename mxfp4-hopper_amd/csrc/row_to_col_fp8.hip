@@ -490,14 +490,7 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
   const int64_t tiles_m = (M + kTile - 1) / kTile, tiles = tiles_m * ((N + kTile - 1) / kTile);
   // one wave of resident blocks: two 512-thread blocks per CU at this
   // kernel's register use (4 waves per SIMD)
-  static int grid_cap = 0;
-  if (grid_cap == 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    grid_cap = 2 * cus;
-  }
+  const int64_t grid_cap = 2 * (int64_t)current_device_caps().cus;
   const int64_t grid = tiles < grid_cap ? tiles : grid_cap;
   auto kernel = full ? row_to_fp8_col_kernel<true> : row_to_fp8_col_kernel<false>;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
