@@ -479,6 +479,62 @@ def test_row_to_fp8_col_msplit_every_byte(oracle, dev, splits, N):
     np.testing.assert_array_equal(out_s.cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
+def _msplit_sentinel_run(dev, q, s, splits, N, max_len=None):
+    import omo
+    from omo_python_api.mxfp4_dequant import split_metadata
+    M = sum(splits)
+    lens, offs, soffs, ml, rows, srows = split_metadata(splits, dev)
+    out_q = torch.full((M * N,), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    out_s = torch.full((srows, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out_q,
+                                                    out_s, lens, offs, soffs, ml if max_len is None else max_len, 1e-10)
+    torch.cuda.synchronize()
+    return bits_u8(out_q), out_s.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("nsplits,N,seed", [(100, 256, 1), (256, 128, 2), (300, 128, 3), (9, 1056, 4), (5, 96, 5)])
+def test_row_to_fp8_col_msplit_many_splits(oracle, dev, nsplits, N, seed):
+    """Many splits (the grid's first dimension), N % 128 != 0 (a partial
+    column tile), and empty, one-row, whole-tile and ragged splits, into
+    sentinel-filled outputs."""
+    rng = np.random.default_rng(seed)
+    splits = [int(v) for v in rng.choice([0, 1, 17, 128, 129, 200, 255, 256, 300], size=nsplits)]
+    _say("msplit many splits", nsplits, N, sum(splits))
+    M = sum(splits)
+    q, s = payload_from_normal(M, N, seed)
+    got, got_s = _msplit_sentinel_run(dev, q, s, splits, N)
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(got, eo)
+    np.testing.assert_array_equal(got_s, es.view(np.uint32))
+
+
+@pytest.mark.parametrize("N", [256, 1056])
+def test_row_to_fp8_col_msplit_short_max_len(oracle, dev, N):
+    """The reference launches ceil(max_split_len / 128) row tiles per split
+    (code/kernel/per_token_Mxfp4RowToBf16ToFp8Col_msplit.cu:256): with a
+    max_split_len below a split's length, that split's rows past those tiles
+    and their scale rows are left as they were."""
+    splits, max_len = [300, 50, 260, 129], 200
+    _say("msplit short max_split_len", splits, N, max_len)
+    M = sum(splits)
+    q, s = payload_from_normal(M, N, 7)
+    got, got_s = _msplit_sentinel_run(dev, q, s, splits, N, max_len)
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    eo, es = eo.copy(), es.view(np.uint32).copy()
+    nan_bits = np.array([np.nan], dtype=np.float32).view(np.uint32)[0]
+    tmax = (max_len + 127) // 128
+    off, soff = 0, 0
+    for m in splits:
+        if m > tmax * 128:
+            blk = eo[off * N:(off + m) * N].reshape(N, m)
+            blk[:, tmax * 128:] = 0xAB
+            es[soff + tmax:soff + (m + 127) // 128] = nan_bits
+        off += m
+        soff += (m + 127) // 128
+    np.testing.assert_array_equal(got, eo)
+    np.testing.assert_array_equal(got_s, es)
+
+
 # ------------------------------------------------------------- dual layout
 @pytest.mark.parametrize("M,K,seed", [(32, 32, 1), (64, 7168, 2), (96, 1056, 3), (256, 256, 4)])
 def test_dual_layout(oracle, dev, M, K, seed):
