@@ -97,7 +97,7 @@ __device__ __forceinline__ uint2 quant_half16_ref(const uint32_t (&p)[8], float 
 __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
                                           uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
                                           uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_m,
-                                          int logical, float eps, int c_eps, uint8_t* tile) {
+                                          int logical, float eps, int c_eps, uint8_t* tile, uint8_t* rs_tile) {
   const int t = threadIdx.x;
   const int64_t mt = logical % tiles_m, kt = logical / tiles_m;
   const int64_t m0 = mt * kDualRows, k0 = kt * kDualCols;
@@ -115,7 +115,6 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
   }
   const bool quad_leader = (t & 3) == 0;
   uint32_t* rq = row_q + (m0 + r0) * (K / 8) + col / 8;
-  uint8_t* rs = row_s + (m0 + r0) * (K / 32) + col / 32;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     // row r0 + 16k is in 16-row band k: its chunks are stored XORed by 4k,
@@ -128,18 +127,29 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
     } else {
       quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
     }
-    if (r0 + 16 * k < rows_valid && col < K) {
-      __builtin_nontemporal_store(codes, rq + k * 2 * K);  // 16 rows down
-      if (quad_leader) rs[k * (K / 2)] = (uint8_t)byte;
-    }
+    if (r0 + 16 * k < rows_valid && col < K) __builtin_nontemporal_store(codes, rq + k * 2 * K);  // 16 rows down
+    // the 8 scale bytes of a tile row are gathered in LDS and leave as one store
+    if (quad_leader) rs_tile[(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)byte;
   }
   __syncthreads();
+  if (t < rows_valid) {
+    uint8_t* rs = row_s + (m0 + t) * (K / 32) + k0 / 32;
+    const int nsc = (int)((K - k0) / 32 < 8 ? (K - k0) / 32 : 8);
+    if (nsc == 8 && (reinterpret_cast<uintptr_t>(rs) & 7) == 0) {
+      *reinterpret_cast<uint2*>(rs) = *reinterpret_cast<const uint2*>(rs_tile + t * 8);
+    } else {
+      for (int j = 0; j < nsc; j++) rs[j] = rs_tile[t * 8 + j];
+    }
+  }
   // ---- columnwise: lanes 4i..4i+3 own column pair i; lane 4i + 2g + h holds
   // rows 32g + 16h .. +15 (half h of row block g), so the four lanes' 8 B
   // code stores form the column's 32 B piece
   const int h = t & 1, g = (t >> 1) & 1, p = t >> 2;
   const int64_t kc = k0 + 2 * p;
-  if (32 * g >= rows_valid || kc >= K) return;
+  // every lane runs the column pass (rows and columns past the tensor read
+  // the tile's clamped copies) so that the scale exchange below sees all
+  // lanes; only valid results are stored
+  const bool active = 32 * g < rows_valid && kc < K;
   const int band = 2 * g + h;
   const int pp = 4 * (p ^ (band << 4));
   uint32_t ca[8], cb[8];
@@ -164,12 +174,24 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
   if (__builtin_expect(amax_b < 0x7F80u, 1)) qb = quant_half16_fast(cb, amax_b, eps, c_eps, &byte_b);
   else qb = quant_half16_ref(cb, eps, &byte_b);
   const int64_t mo = (m0 + 16 * band) / 2;
-  *reinterpret_cast<uint2*>(col_q + kc * (M / 2) + mo) = qa;
-  *reinterpret_cast<uint2*>(col_q + (kc + 1) * (M / 2) + mo) = qb;
-  if (h == 0) {
-    const int64_t so = (m0 + 32 * g) / 32;
-    col_s[kc * (M / 32) + so] = (uint8_t)byte_a;
-    col_s[(kc + 1) * (M / 32) + so] = (uint8_t)byte_b;
+  if (active) {
+    *reinterpret_cast<uint2*>(col_q + kc * (M / 2) + mo) = qa;
+    *reinterpret_cast<uint2*>(col_q + (kc + 1) * (M / 2) + mo) = qb;
+  }
+  // A column's two scale bytes of this tile (row blocks g = 0, 1) sit in
+  // lanes 4p + 2g; swapping them (quad lane ^ 2) lets lane 4p write column
+  // kc's pair and lane 4p + 2 column kc + 1's as one 2-byte store each.
+  const uint32_t oa = dpp_quad_xor2(byte_a), ob = dpp_quad_xor2(byte_b);
+  if (h == 0 && kc < K) {
+    const int64_t so = m0 / 32;  // even: m0 is a multiple of 64
+    uint8_t* const cs = col_s + (kc + g) * (M / 32) + so;
+    if (rows_valid == kDualRows && (M / 32) % 2 == 0 && (reinterpret_cast<uintptr_t>(col_s) & 1) == 0) {
+      const uint32_t pair = g == 0 ? (byte_a | (oa << 8)) : (ob | (byte_b << 8));
+      *reinterpret_cast<uint16_t*>(cs) = (uint16_t)pair;
+    } else if (active) {
+      col_s[kc * (M / 32) + so + g] = (uint8_t)byte_a;
+      col_s[(kc + 1) * (M / 32) + so + g] = (uint8_t)byte_b;
+    }
   }
 }
 
@@ -178,10 +200,11 @@ __global__ __launch_bounds__(kDualThreads) void quant_dual_kernel(const uint16_t
                                                          uint8_t* __restrict__ col_s, int64_t M, int64_t K,
                                                          int tiles_m, int tiles, int per_xcd, float eps, int c_eps) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+  __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
   const int b = blockIdx.x;
   const int logical = (b % kXcds) * per_xcd + b / kXcds;
   if (logical >= tiles) return;
-  dual_tile(x, row_q, row_s, col_q, col_s, M, K, tiles_m, logical, eps, c_eps, tile);
+  dual_tile(x, row_q, row_s, col_q, col_s, M, K, tiles_m, logical, eps, c_eps, tile, rs_tile);
 }
 
 // Grouped form: one launch over up to kDualGroupMax tensors (e.g. the weights
@@ -206,6 +229,7 @@ struct DualGroup {
 
 __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const DualGroup g) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+  __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
   const int b = blockIdx.x;
   const int logical = (b % kXcds) * g.per_xcd + b / kXcds;
   if (logical >= g.tiles) return;
@@ -213,7 +237,7 @@ __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const 
   while (i + 1 < g.count && logical >= g.item[i + 1].tile_begin) i++;
   const DualItem& it = g.item[i];
   dual_tile(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, it.tiles_m, logical - it.tile_begin, g.eps,
-            g.c_eps, tile);
+            g.c_eps, tile, rs_tile);
 }
 
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
