@@ -554,11 +554,13 @@ def test_dual_layout(oracle, dev, M, K, seed):
     np.testing.assert_array_equal(bits_u8(cs).reshape(-1), est)
 
 
-@pytest.mark.parametrize("M,K,seed", [(96, 1056, 5), (192, 7168, 6), (64, 32, 7)])
+@pytest.mark.parametrize("M,K,seed", [(96, 1056, 5), (192, 7168, 6), (64, 32, 7), (576, 512, 8), (448, 768, 9),
+                                      (1024, 256, 10), (320, 7168, 11)])
 def test_dual_layout_every_byte_special_columns(oracle, dev, M, K, seed):
     """Special-value blocks placed down columns (inside the second 16-row half
     of a 32-row block, and across two blocks), outputs pre-filled with a
-    sentinel so every byte must be written."""
+    sentinel so every byte must be written; shapes of several tile rows and
+    columns, with and without a ragged 32-row last tile row."""
     import omo
     _say("dual every byte", M, K)
     x = (torch.randn((M, K), generator=torch.Generator().manual_seed(seed)) * 3).to(torch.bfloat16)
