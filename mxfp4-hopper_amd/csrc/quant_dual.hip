@@ -195,6 +195,151 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
   }
 }
 
+// ---- four tiles per workgroup, for M % 64 == 0 and K % 256 == 0
+//
+// A workgroup quantizes the (up to) four vertically adjacent 64 x 256 tiles
+// of a 256-row super-tile one after the other, as dual_tile does, but keeps
+// each lane's transposed-code pieces (8 B per column and tile) and column
+// scale pairs in registers. After the last tile the four lanes of a column
+// pair (bands b = 0..3) transpose their 4 x 4 pieces (two DPP butterflies),
+// so lane b holds tile b's 32 B of each of its two columns and writes them
+// as two 16 B stores: a column's 128 B line takes two store requests instead
+// of four, and its 8 scale bytes one 8-byte store instead of four 2-byte
+// ones (a CU issues one request per cache line a store instruction touches).
+constexpr int kSuperSteps = 4;
+constexpr int kSuperRows = kDualRows * kSuperSteps;  // 256
+
+__device__ __forceinline__ uint2 dpp_quad_xor2_u2(uint2 v) { return make_uint2(dpp_quad_xor2(v.x), dpp_quad_xor2(v.y)); }
+__device__ __forceinline__ uint2 dpp_quad_xor1_u2(uint2 v) { return make_uint2(dpp_quad_xor1(v.x), dpp_quad_xor1(v.y)); }
+
+// Lane b (of a quad) holds e[s] = piece (b, s); afterwards e[s] = piece (s, b).
+__device__ __forceinline__ void quad_transpose4(uint2 (&e)[4], int b) {
+  uint2 o[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) o[s] = dpp_quad_xor2_u2(e[s ^ 2]);  // lane b ^ 2's piece s ^ 2
+#pragma unroll
+  for (int s = 0; s < 4; s++)
+    if ((s & 2) != (b & 2)) e[s] = o[s];
+#pragma unroll
+  for (int s = 0; s < 4; s++) o[s] = dpp_quad_xor1_u2(e[s ^ 1]);  // lane b ^ 1's piece s ^ 1
+#pragma unroll
+  for (int s = 0; s < 4; s++)
+    if ((s & 1) != (b & 1)) e[s] = o[s];
+}
+
+__device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
+                                            uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
+                                            uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms,
+                                            int logical, float eps, int c_eps, uint8_t* tile, uint8_t* rs_tile) {
+  const int t = threadIdx.x;
+  const int64_t m0s = (int64_t)(logical % tiles_ms) * kSuperRows, k0 = (int64_t)(logical / tiles_ms) * kDualCols;
+  const int steps = (int)((M - m0s) / kDualRows < kSuperSteps ? (M - m0s) / kDualRows : kSuperSteps);
+  const int r0 = t >> 5, cc = t & 31;
+  const bool quad_leader = (t & 3) == 0;
+  const int h = t & 1, g = (t >> 1) & 1, p = t >> 2;
+  const int band = 2 * g + h;
+  const int pp = 4 * (p ^ (band << 4));
+  const int64_t kc = k0 + 2 * p;
+  const bool rs_vec = (reinterpret_cast<uintptr_t>(row_s) & 7) == 0;
+  uint2 acc_a[4], acc_b[4];  // [tile] -> this lane's 8 B of columns kc, kc + 1
+#pragma unroll
+  for (int s = 0; s < 4; s++) acc_a[s] = acc_b[s] = make_uint2(0u, 0u);
+  uint32_t sc_lo = 0, sc_hi = 0;  // scale pairs of column kc + g, tile s at bytes 2s, 2s + 1
+  for (int st = 0; st < steps; st++) {
+    const int64_t m0 = m0s + st * kDualRows;
+    const uint16_t* src = x + (m0 + r0) * K + k0 + cc * 8;
+    u32x4 d[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) d[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16 * k * K));
+    uint32_t* rq = row_q + (m0 + r0) * (K / 8) + k0 / 8 + cc;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      *reinterpret_cast<u32x4*>(tile + (r0 + 16 * k) * kDualPitch + ((cc ^ (k << 2)) * 16)) = d[k];
+      uint32_t codes, byte;
+      const uint32_t am = quad_max_u32(chunk_absmax_bits(d[k]));
+      if (__builtin_expect(am < 0x7F80u, 1)) {
+        codes = quant_chunk_fast(d[k], am, eps, c_eps, &byte);
+      } else {
+        quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
+      }
+      __builtin_nontemporal_store(codes, rq + k * 2 * K);
+      if (quad_leader) rs_tile[(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)byte;
+    }
+    __syncthreads();
+    if (t < kDualRows) {
+      uint8_t* rs = row_s + (m0 + t) * (K / 32) + k0 / 32;
+      if (rs_vec) {
+        *reinterpret_cast<uint2*>(rs) = *reinterpret_cast<const uint2*>(rs_tile + t * 8);
+      } else {
+        for (int j = 0; j < 8; j++) rs[j] = rs_tile[t * 8 + j];
+      }
+    }
+    uint32_t ca[8], cb[8];
+    uint32_t amax_a = 0, amax_b = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t w0 = *reinterpret_cast<const uint32_t*>(tile + (16 * band + 2 * j) * kDualPitch + pp);
+      const uint32_t w1 = *reinterpret_cast<const uint32_t*>(tile + (16 * band + 2 * j + 1) * kDualPitch + pp);
+      ca[j] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+      cb[j] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+      amax_a = pk_max_u16(amax_a, ca[j] & 0x7FFF7FFFu);
+      amax_b = pk_max_u16(amax_b, cb[j] & 0x7FFF7FFFu);
+    }
+    amax_a = max(amax_a & 0xFFFFu, amax_a >> 16);
+    amax_b = max(amax_b & 0xFFFFu, amax_b >> 16);
+    amax_a = max(amax_a, dpp_quad_xor1(amax_a));
+    amax_b = max(amax_b, dpp_quad_xor1(amax_b));
+    uint32_t byte_a, byte_b;
+    uint2 qa, qb;
+    if (__builtin_expect(amax_a < 0x7F80u, 1)) qa = quant_half16_fast(ca, amax_a, eps, c_eps, &byte_a);
+    else qa = quant_half16_ref(ca, eps, &byte_a);
+    if (__builtin_expect(amax_b < 0x7F80u, 1)) qb = quant_half16_fast(cb, amax_b, eps, c_eps, &byte_b);
+    else qb = quant_half16_ref(cb, eps, &byte_b);
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      if (s == st) {
+        acc_a[s] = qa;
+        acc_b[s] = qb;
+      }
+    }
+    const uint32_t oa = dpp_quad_xor2(byte_a), ob = dpp_quad_xor2(byte_b);
+    const uint32_t pair = g == 0 ? (byte_a | (oa << 8)) : (ob | (byte_b << 8));
+    if (st < 2) sc_lo |= pair << (16 * st);
+    else sc_hi |= pair << (16 * (st - 2));
+    __syncthreads();  // this tile's LDS reads are done before the next tile's writes
+  }
+  quad_transpose4(acc_a, band);
+  quad_transpose4(acc_b, band);
+  if (band < steps) {  // lane b: tile b's 32 B of columns kc and kc + 1
+    uint8_t* da = col_q + kc * (M / 2) + m0s / 2 + 32 * band;
+    uint8_t* db = da + M / 2;
+    *reinterpret_cast<u32x4*>(da) = u32x4{acc_a[0].x, acc_a[0].y, acc_a[1].x, acc_a[1].y};
+    *reinterpret_cast<u32x4*>(da + 16) = u32x4{acc_a[2].x, acc_a[2].y, acc_a[3].x, acc_a[3].y};
+    *reinterpret_cast<u32x4*>(db) = u32x4{acc_b[0].x, acc_b[0].y, acc_b[1].x, acc_b[1].y};
+    *reinterpret_cast<u32x4*>(db + 16) = u32x4{acc_b[2].x, acc_b[2].y, acc_b[3].x, acc_b[3].y};
+  }
+  if (h == 0) {  // lane g: column kc + g's scale bytes of the super-tile
+    uint8_t* cs = col_s + (kc + g) * (M / 32) + m0s / 32;
+    if (steps == kSuperSteps && (reinterpret_cast<uintptr_t>(cs) & 7) == 0) {
+      *reinterpret_cast<uint2*>(cs) = make_uint2(sc_lo, sc_hi);
+    } else {
+      for (int j = 0; j < 2 * steps; j++) cs[j] = (uint8_t)((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3)));
+    }
+  }
+}
+
+__global__ __launch_bounds__(kDualThreads) void quant_dual_super_kernel(
+    const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q, uint8_t* __restrict__ row_s,
+    uint8_t* __restrict__ col_q, uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms, int tiles,
+    int per_xcd, float eps, int c_eps) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+  __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
+  const int b = blockIdx.x;
+  const int logical = (b % kXcds) * per_xcd + b / kXcds;
+  if (logical >= tiles) return;
+  dual_super4(x, row_q, row_s, col_q, col_s, M, K, tiles_ms, logical, eps, c_eps, tile, rs_tile);
+}
+
 __global__ __launch_bounds__(kDualThreads) void quant_dual_kernel(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
                                                          uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
                                                          uint8_t* __restrict__ col_s, int64_t M, int64_t K,
@@ -240,12 +385,42 @@ __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const 
             g.c_eps, tile, rs_tile);
 }
 
+// Grouped form of quant_dual_super_kernel: every item has M % 64 == 0,
+// K % 256 == 0 and aligned buffers; tiles_m and tile_begin count super-tiles.
+__global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_super_kernel(const DualGroup g) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+  __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
+  const int b = blockIdx.x;
+  const int logical = (b % kXcds) * g.per_xcd + b / kXcds;
+  if (logical >= g.tiles) return;
+  int i = 0;
+  while (i + 1 < g.count && logical >= g.item[i + 1].tile_begin) i++;
+  const DualItem& it = g.item[i];
+  dual_super4(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, it.tiles_m, logical - it.tile_begin, g.eps,
+              g.c_eps, tile, rs_tile);
+}
+
+// Shapes and buffers the four-tile kernels take: whole 64 x 256 tiles, 16 B
+// aligned input and transposed codes, dword-aligned rowwise codes.
+static bool dual_super_ok(const void* x, const void* row_q, const void* col_q, int64_t M, int64_t K) {
+  return M % kDualRows == 0 && K % kDualCols == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(row_q) & 3) == 0 && (reinterpret_cast<uintptr_t>(col_q) & 15) == 0;
+}
+
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
                              float eps, hipStream_t stream) {
   if (M == 0 || K == 0) return hipSuccess;
   const int64_t tiles_m = (M + kDualRows - 1) / kDualRows;
   const int64_t tiles_k = (K + kDualCols - 1) / kDualCols;
   const int64_t tiles = tiles_m * tiles_k;
+  if (dual_super_ok(x, row_q, col_q, M, K)) {
+    const int64_t sm = (M + kSuperRows - 1) / kSuperRows, st = sm * tiles_k, spx = (st + kXcds - 1) / kXcds;
+    hipLaunchKernelGGL(quant_dual_super_kernel, dim3((unsigned)(spx * kXcds)), dim3(kDualThreads), 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
+                       static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, (int)sm, (int)st, (int)spx,
+                       eps, host_c_eps(eps, 6.0f));
+    return hipGetLastError();
+  }
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
   hipLaunchKernelGGL(quant_dual_kernel, dim3((unsigned)(per_xcd * kXcds)), dim3(kDualThreads), 0, stream,
                      static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
@@ -259,6 +434,12 @@ hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps
     DualGroup g;
     memset(&g, 0, sizeof(g));
     g.count = count - base < kDualGroupMax ? count - base : kDualGroupMax;
+    bool super = true;
+    for (int j = 0; j < g.count; j++) {
+      const DualSpec& d = items[base + j];
+      super = super && (d.M == 0 || d.K == 0 || dual_super_ok(d.x, d.row_q, d.col_q, d.M, d.K));
+    }
+    const int unit_rows = super ? kSuperRows : kDualRows;
     int tiles = 0;
     for (int j = 0; j < g.count; j++) {
       const DualSpec& d = items[base + j];
@@ -270,7 +451,7 @@ hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps
       it.col_s = static_cast<uint8_t*>(d.col_s);
       it.M = d.M;
       it.K = d.K;
-      it.tiles_m = (int)((d.M + kDualRows - 1) / kDualRows);
+      it.tiles_m = (int)((d.M + unit_rows - 1) / unit_rows);
       it.tile_begin = tiles;
       tiles += (d.M == 0 || d.K == 0) ? 0 : it.tiles_m * (int)((d.K + kDualCols - 1) / kDualCols);
     }
@@ -279,7 +460,13 @@ hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps
     g.per_xcd = (tiles + kXcds - 1) / kXcds;
     g.eps = eps;
     g.c_eps = host_c_eps(eps, 6.0f);
-    hipLaunchKernelGGL(quant_dual_grouped_kernel, dim3((unsigned)(g.per_xcd * kXcds)), dim3(kDualThreads), 0, stream, g);
+    if (super) {
+      hipLaunchKernelGGL(quant_dual_grouped_super_kernel, dim3((unsigned)(g.per_xcd * kXcds)), dim3(kDualThreads), 0,
+                         stream, g);
+    } else {
+      hipLaunchKernelGGL(quant_dual_grouped_kernel, dim3((unsigned)(g.per_xcd * kXcds)), dim3(kDualThreads), 0, stream,
+                         g);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
