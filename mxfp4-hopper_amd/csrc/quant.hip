@@ -237,10 +237,11 @@ hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, 
   // Two-phase kernel when each workgroup's share (a multiple of 64 chunks,
   // 16 B of scale bytes) is at least 4096 chunks, fits its LDS in one round
   // (4 B of codes + 1/4 B of scale per chunk), and fills its steps of 2048
-  // chunks to at least 95%: a step costs about one load latency however full
-  // it is, so a share of 8.03 steps takes as long as 9 (measured: 16431 x
-  // 2048 ran 7% slower two-phase). Several rounds per workgroup (alternating
-  // read and write phases) measured 6-12% slower than quant_rowwise_kernel.
+  // chunks to at least 95%. Measured where it does not: 16431 x 2048 (8.03
+  // steps per CU) and 16431 x 4096 (16.06) ran 6-8% slower two-phase than
+  // quant_rowwise_kernel, both in 9 / 17 steps and with the surplus chunks
+  // loaded alongside the first step (8 / 16 steps); several rounds per
+  // workgroup (alternating read and write phases) measured 6-12% slower.
   const int64_t share = ((a.nchunks + dc.cus - 1) / dc.cus + 63) / 64 * 64;
   const int64_t cap = (int64_t)dc.lds_per_workgroup * 4 / 17 / 64 * 64;
   const int64_t steps = (share + kPhThreads * kPhUnroll - 1) / (kPhThreads * kPhUnroll);
