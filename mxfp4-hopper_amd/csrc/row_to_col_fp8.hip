@@ -242,29 +242,49 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
     out_s_row[2 * p + 1] = inv1;
   }
   uint32_t w0[4] = {0u, 0u, 0u, 0u}, w1[4] = {0u, 0u, 0u, 0u};
-  // Dense: |v| <= amax and m = fl(448 / amax) bound |v * m| by 448 (1 + 2^-23),
-  // which E4M3 RNE rounds to 448 (only |x| > 464 overflows), so the clamp of
-  // the reference changes no byte. Grouped: the multiplier is a power of two
-  // that can exceed 448 / amax when amax <= eps, so the clamp stays; it needs
-  // finite multipliers to be NaN-free.
-  if (fast && (!MSPLIT || (m0 < __builtin_inff() && m1 < __builtin_inff()))) {
+  // The reference clamps v * m to +-448 before the E4M3 conversion. Where
+  // |v * m| <= 448 (1 + 2^-23), which E4M3 RNE rounds to at most 448 (only
+  // |x| > 464 overflows), the clamp changes no byte and is left out:
+  //  * dense: |v| <= amax and m = fl(448 / amax);
+  //  * grouped, amax > eps: m = 2^-k with 2^k the smallest power of two at
+  //    or above fl(amax / 448); amax = c * 2^j for an E2M1 magnitude c, so
+  //    amax / 448 = (c / 7) 2^(j - 6) is never within rounding distance of a
+  //    power of two, 2^k >= amax / 448 exactly and |v * m| <= 448;
+  //  * grouped, amax <= eps: m = 1, so the bound needs amax <= 448.
+  // Otherwise (grouped with amax in (448, eps]) the clamp stays; a grouped
+  // tile also needs finite multipliers to be NaN-free here.
+  const bool finite_m = !MSPLIT || (m0 < __builtin_inff() && m1 < __builtin_inff());
+  const bool no_clamp = !MSPLIT || ((a0 > eps || a0 <= 448.0f) && (a1 > eps || a1 <= 448.0f));
+  if (fast && finite_m) {
+    if (no_clamp) {
 #pragma unroll
-    for (int j4 = 0; j4 < 4; j4++) {
-      float x[4], y[4];  // rows 4 j4 + k of columns 2p (x), 2p + 1 (y)
+      for (int j4 = 0; j4 < 4; j4++) {
+        float x[4], y[4];  // rows 4 j4 + k of columns 2p (x), 2p + 1 (y)
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float v0, v1;
-        cvt_pk_f32_fp4<0>(cb[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
-        x[k] = v0 * m0;
-        y[k] = v1 * m1;
-        if (MSPLIT) {
-          x[k] = __builtin_amdgcn_fmed3f(x[k], -448.0f, 448.0f);
-          y[k] = __builtin_amdgcn_fmed3f(y[k], -448.0f, 448.0f);
+        for (int k = 0; k < 4; k++) {
+          float v0, v1;
+          cvt_pk_f32_fp4<0>(cb[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
+          x[k] = v0 * m0;
+          y[k] = v1 * m1;
         }
+        // bytes 0, 1 from the low-word convert, bytes 2, 3 from the high-word one
+        w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
+        w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
       }
-      // bytes 0, 1 from the low-word convert, bytes 2, 3 from the high-word one
-      w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
-      w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+    } else {
+#pragma unroll
+      for (int j4 = 0; j4 < 4; j4++) {
+        float x[4], y[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          float v0, v1;
+          cvt_pk_f32_fp4<0>(cb[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
+          x[k] = __builtin_amdgcn_fmed3f(v0 * m0, -448.0f, 448.0f);
+          y[k] = __builtin_amdgcn_fmed3f(v1 * m1, -448.0f, 448.0f);
+        }
+        w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
+        w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+      }
     }
   } else {
 #pragma unroll

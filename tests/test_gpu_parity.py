@@ -535,6 +535,32 @@ def test_row_to_fp8_col_msplit_short_max_len(oracle, dev, N):
     np.testing.assert_array_equal(got_s, es)
 
 
+@pytest.mark.parametrize("eps,smax,mixed", [(1e3, 134, False), (1e5, 140, False), (1e3, 140, True)])
+def test_row_to_fp8_col_msplit_large_eps(oracle, dev, eps, smax, mixed):
+    """A column whose amax does not exceed eps gets multiplier 1 in the
+    grouped rule (code/kernel/per_token_Mxfp4RowToBf16ToFp8Col_msplit.cu:23-43),
+    so its values above 448 reach the clamp: scale bytes up to smax give
+    column maxima up to 6 * 2^(smax - 127), above 448 and at most eps. In the
+    mixed case the first half of the scale blocks stays below 135 (clamped
+    columns) and the second half reaches 140 (columns with amax > eps)."""
+    from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper
+    rng = np.random.default_rng(int(eps))
+    splits, N = [300, 129, 64], 512
+    M = sum(splits)
+    _say("msplit large eps", eps, splits, N)
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(120, smax + 1, size=(M, N // 32)).astype(np.uint8)
+    if mixed:
+        s[:, : N // 64] = rng.integers(120, 135, size=(M, N // 64)).astype(np.uint8)
+    ys, ss = omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev),
+                                                                 splits, eps)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits, eps=eps)
+    assert np.count_nonzero((eo & 0x7F) == 0x7E) > 0  # the clamp to +-448 is exercised
+    np.testing.assert_array_equal(np.concatenate([bits_u8(y).reshape(-1) for y in ys]), eo)
+    np.testing.assert_array_equal(torch.cat(ss).cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
 # ------------------------------------------------------------- dual layout
 @pytest.mark.parametrize("M,K,seed", [(32, 32, 1), (64, 7168, 2), (96, 1056, 3), (256, 256, 4)])
 def test_dual_layout(oracle, dev, M, K, seed):
