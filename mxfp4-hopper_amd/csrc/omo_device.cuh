@@ -111,16 +111,15 @@ __device__ __forceinline__ uint32_t e2m1_from_f32_ref(float q) {
   return ((sign >> 28) | r) & 0xFu;
 }
 
-// cvt_pk_f32_fp4<B>(src, scale, &lo, &hi): the two E2M1 nibbles of byte B
-// of `src` times `scale`, as two fp32 values (exact for scale 2^k).
+// cvt_pk_f32_fp4<0>(src, scale, &lo, &hi): the two E2M1 nibbles of byte 0
+// of `src` times `scale`, as two fp32 values (exact for scale 2^k). Only
+// byte 0 is provided: it is the form the parity tests cover.
 template <int B>
 __device__ __forceinline__ void cvt_pk_f32_fp4(uint32_t src, float scale, float* lo, float* hi) {
+  static_assert(B == 0, "only byte 0 of the source is supported");
   typedef float f32x2_t __attribute__((ext_vector_type(2)));
   f32x2_t r;
-  if constexpr (B == 0) asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2" : "=v"(r) : "v"(src), "v"(scale));
-  else if constexpr (B == 1) asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[1,0,0]" : "=v"(r) : "v"(src), "v"(scale));
-  else if constexpr (B == 2) asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[0,1,0]" : "=v"(r) : "v"(src), "v"(scale));
-  else asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[1,1,0]" : "=v"(r) : "v"(src), "v"(scale));
+  asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2" : "=v"(r) : "v"(src), "v"(scale));
   *lo = r[0];
   *hi = r[1];
 }
