@@ -93,48 +93,57 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(QuantArgs a) {
 constexpr int kPhThreads = 1024;
 constexpr int kPhUnroll = 2;
 
+// Read phase of the two-phase kernels: loads chunks [c0, c0 + n) of a.x (n a
+// multiple of 4, so quads are whole), quantizes them and leaves the code
+// dwords in lds_q[0, n) and the scale bytes in lds_s[0, n / 4). The caller
+// synchronizes before reading them.
+__device__ __forceinline__ void ph_read_phase(const QuantArgs& a, int64_t c0, int n, uint32_t* lds_q, uint8_t* lds_s) {
+  const int t = threadIdx.x;
+  const bool quad_leader = (t & 3) == 0;
+  u32x4 nx[kPhUnroll];
+#pragma unroll
+  for (int u = 0; u < kPhUnroll; u++) {
+    const int i = u * kPhThreads + t;
+    nx[u] = __builtin_nontemporal_load(a.x + c0 + (i < n ? i : 0));
+  }
+  for (int i0 = 0; i0 < n; i0 += kPhThreads * kPhUnroll) {
+    u32x4 d[kPhUnroll];
+#pragma unroll
+    for (int u = 0; u < kPhUnroll; u++) d[u] = nx[u];
+    // the next step's loads (past the end: a reload of chunk 0, unused)
+#pragma unroll
+    for (int u = 0; u < kPhUnroll; u++) {
+      const int i = i0 + kPhThreads * kPhUnroll + u * kPhThreads + t;
+      nx[u] = __builtin_nontemporal_load(a.x + c0 + (i < n ? i : 0));
+    }
+#pragma unroll
+    for (int u = 0; u < kPhUnroll; u++) {
+      const int i = i0 + u * kPhThreads + t;
+      if (i >= n) continue;
+      uint32_t codes, byte;
+      const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
+      if (__builtin_expect(am < 0x7F80u, 1)) {
+        codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
+      } else {
+        quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
+      }
+      lds_q[i] = codes;
+      if (quad_leader) lds_s[i >> 2] = (uint8_t)byte;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kPhThreads) void quant_phased_kernel(QuantArgs a, int64_t share, int round) {
   extern __shared__ __attribute__((aligned(16))) uint32_t ph_lds[];  // round code dwords, then round/4 scale bytes
   uint8_t* lsc = reinterpret_cast<uint8_t*>(ph_lds + round);
   const int t = threadIdx.x;
-  const bool quad_leader = (t & 3) == 0;
   const int64_t wg_begin = (int64_t)blockIdx.x * share;
   const int64_t wg_end = wg_begin + share < a.nchunks ? wg_begin + share : a.nchunks;
   for (int64_t r0 = wg_begin; r0 < wg_end; r0 += round) {
     // chunks of this round: a multiple of 4, so quads are whole
     const int n = (int)(wg_end - r0 < round ? wg_end - r0 : round);
     if (r0 != wg_begin) __syncthreads();  // the previous round's LDS reads are done
-    u32x4 nx[kPhUnroll];
-#pragma unroll
-    for (int u = 0; u < kPhUnroll; u++) {
-      const int i = u * kPhThreads + t;
-      nx[u] = __builtin_nontemporal_load(a.x + r0 + (i < n ? i : 0));
-    }
-    for (int i0 = 0; i0 < n; i0 += kPhThreads * kPhUnroll) {
-      u32x4 d[kPhUnroll];
-#pragma unroll
-      for (int u = 0; u < kPhUnroll; u++) d[u] = nx[u];
-      // the next step's loads (past the end: a reload of chunk 0, unused)
-#pragma unroll
-      for (int u = 0; u < kPhUnroll; u++) {
-        const int i = i0 + kPhThreads * kPhUnroll + u * kPhThreads + t;
-        nx[u] = __builtin_nontemporal_load(a.x + r0 + (i < n ? i : 0));
-      }
-#pragma unroll
-      for (int u = 0; u < kPhUnroll; u++) {
-        const int i = i0 + u * kPhThreads + t;
-        if (i >= n) continue;
-        uint32_t codes, byte;
-        const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
-        if (__builtin_expect(am < 0x7F80u, 1)) {
-          codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
-        } else {
-          quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
-        }
-        ph_lds[i] = codes;
-        if (quad_leader) lsc[i >> 2] = (uint8_t)byte;
-      }
-    }
+    ph_read_phase(a, r0, n, ph_lds, lsc);
     __syncthreads();
     for (int i = 4 * t; i < n; i += 4 * kPhThreads)
       __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&ph_lds[i]), reinterpret_cast<u32x4*>(a.q + r0 + i));
@@ -199,6 +208,34 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantRowsArgs a) {
   }
 }
 
+// Two-phase form of the payload rows [codes (K/2 B) | scales (K/32 B)],
+// stride 17K/32 B, for K % 512 == 0 (whole 16 B pieces per row) and 16 B
+// aligned buffers: workgroup b takes rows [b * rpw, b * rpw + rpw), whose
+// chunks are contiguous in the input and whose payload rows are contiguous
+// in the output. The read phase converts them into LDS as in
+// quant_phased_kernel; the write phase then covers the output region with
+// 16 B stores, piece j of a row coming from the row's code dwords for
+// j < K/32 and from its scale bytes after that.
+__global__ __launch_bounds__(kPhThreads) void quant_phased_rows_kernel(QuantArgs a, uint8_t* __restrict__ out,
+                                                                       int64_t rows, int rpw, int cpr) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t ph_lds[];  // rpw * cpr code dwords, then scale bytes
+  uint8_t* lsc = reinterpret_cast<uint8_t*>(ph_lds + (int64_t)rpw * cpr);
+  const int64_t row0 = (int64_t)blockIdx.x * rpw;
+  const int nrows = (int)(rows - row0 < rpw ? rows - row0 : rpw);
+  ph_read_phase(a, row0 * cpr, nrows * cpr, ph_lds, lsc);
+  __syncthreads();
+  const int cq = cpr / 4;          // 16 B pieces of codes per row
+  const int ppr = cq + cpr / 64;   // 16 B pieces per payload row
+  u32x4* dst = reinterpret_cast<u32x4*>(out + row0 * (int64_t)ppr * 16);
+  for (int i = threadIdx.x; i < nrows * ppr; i += kPhThreads) {
+    const int r = i / ppr;
+    const int j = i - r * ppr;
+    const u32x4* src = j < cq ? reinterpret_cast<const u32x4*>(ph_lds + r * cpr) + j
+                              : reinterpret_cast<const u32x4*>(lsc + r * (cpr / 4)) + (j - cq);
+    __builtin_nontemporal_store(*src, dst + i);
+  }
+}
+
 hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, int64_t s_stride, int64_t rows,
                              int64_t K, float eps, hipStream_t stream) {
   if (rows == 0 || K == 0) return hipSuccess;
@@ -213,6 +250,37 @@ hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, 
   a.bpr = (int)((K / 8 + 256 * U - 1) / (256 * U));
   a.eps = eps;
   a.c_eps = host_c_eps(eps, 6.0f);
+  // Payload rows (scales right after the codes, one stride) take the
+  // two-phase kernel when rpw whole rows per workgroup give every CU a share
+  // of at least 4096 chunks that fits its LDS and fills the 2048-chunk steps
+  // to at least 95%, the conditions under which quant_phased_kernel wins.
+  const int64_t stride = K / 32 * 17;
+  const bool packed = q_stride == stride && s_stride == stride && static_cast<uint8_t*>(s) == a.q + K / 2;
+  const bool aligned16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q)) & 15) == 0;
+  if (packed && aligned16 && K % 512 == 0) {
+    const DeviceCaps dc = current_device_caps();
+    const int64_t cpr = K / 8;
+    const int64_t rpw = (rows + dc.cus - 1) / dc.cus;
+    const int64_t grid = (rows + rpw - 1) / rpw;
+    const int64_t share = rpw * cpr;
+    const int64_t steps = (share + kPhThreads * kPhUnroll - 1) / (kPhThreads * kPhUnroll);
+    const double fill = (double)(rows * cpr) / ((double)grid * kPhThreads * kPhUnroll * (double)steps);
+    const int64_t lds = share * 4 + share / 4;
+    if (share >= 4096 && lds <= dc.lds_per_workgroup && fill >= 0.95 && grid >= dc.cus / 2) {
+      QuantArgs p;
+      p.x = static_cast<const u32x4*>(x);
+      p.q = nullptr;
+      p.s = nullptr;
+      p.nchunks = rows * cpr;
+      p.eps = eps;
+      p.fp4_min = -6.0f;
+      p.fp4_max = 6.0f;
+      p.c_eps = a.c_eps;
+      hipLaunchKernelGGL(quant_phased_rows_kernel, dim3((unsigned)grid), dim3(kPhThreads), (size_t)lds, stream, p,
+                         a.q, rows, (int)rpw, (int)cpr);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((quant_rows_kernel<U>), dim3((unsigned)(rows * a.bpr)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
