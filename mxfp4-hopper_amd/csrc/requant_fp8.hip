@@ -192,12 +192,17 @@ hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* o
 // block in LDS by restating the reference rule for every entry. Each lane
 // then needs one 8-byte table row per tile row and v_perm_b32 lookups.
 //
-// Lane mapping (as in the row -> column FP8 kernel): lane t owns code-byte
-// column p (element columns 2p, 2p+1) and rows 16q .. 16q+15, q = t % 8; the
-// 8 lanes of a column write its 128 output rows as one full 128 B line per
-// store instruction. Four passes cover the tile's 128 byte columns.
+// Lane mapping: lane t owns code bytes 4c .. 4c+3 (element columns 8c ..
+// 8c+7, one MX column), c = t / 8, and rows 16q .. 16q+15, q = t % 8; the 8
+// lanes of a code dword write its 8 element columns' 128 output rows as one
+// full 128 B line each per store instruction. Per row a lane reads one code
+// dword and one 8-byte table row; the magnitudes of the four low nibbles
+// (cw & 0x07070707) and of the four high nibbles ((cw >> 4) & 0x07070707)
+// are the v_perm_b32 selectors that look up the four even and the four odd
+// element columns' bytes, and 4x4 byte transposes (eight v_perm_b32 each)
+// turn four rows of those into 4-row pieces of the output columns.
 constexpr int kColTile = 128;
-constexpr int kColPitch = kColTile + 16;  // 16 B aligned LDS rows
+constexpr int kColPitch = kColTile + 32;  // 16 B aligned LDS rows; 40 dwords keep a wave's row reads on distinct banks
 
 struct ColSmem {
   uint8_t codes[kColTile * kColPitch];
@@ -269,37 +274,38 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_col_kernel(const uint8_t* __
   __syncthreads();
   // scale row of the tile: 256 floats, entry e holds MX column e / 32 (:210-212)
   __builtin_nontemporal_store(__uint_as_float(sm.gpart[t >> 5][0] << 23), out_s + by * (Kb * 2) + bx * 256 + t);
-  const int qq = t & 7;
-#pragma unroll 1
-  for (int pass = 0; pass < 4; pass++) {
-    const int p = 32 * pass + (t >> 3), cblk = p >> 4;
-    const uint32_t g = sm.gpart[cblk][0];
-    uint32_t r[16];
+  const int qq = t & 7, cg = t >> 3, mx = cg >> 2;
+  const uint32_t g = sm.gpart[mx][0];
+  const u32x4 sw = *reinterpret_cast<const u32x4*>(&sm.scales[mx][16 * qq]);
+  u32x4 col[8];  // element column 8cg + k: rows 16qq + 4a .. 16qq + 4a + 3 in dword a
 #pragma unroll
-    for (int j4 = 0; j4 < 4; j4++) {
-      const uint32_t sw = *reinterpret_cast<const uint32_t*>(&sm.scales[cblk][16 * qq + 4 * j4]);
+  for (int a = 0; a < 4; a++) {
+    uint32_t ev[4], od[4];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int j = 4 * j4 + k;
-        const uint32_t adj = (g - ((sw >> (8 * k)) & 0xFFu)) & 0xFFu;
-        const uint32_t cb = sm.codes[col_lds_row(16 * qq + j) * kColPitch + p];
-        const u32x2 tr = *reinterpret_cast<const u32x2*>(&sm.table[adj][0]);
-        // byte 0: element column 2p (low nibble), byte 1: 2p + 1 (high nibble)
-        const uint32_t sel = (cb & 0x7u) | ((cb << 4) & 0x700u) | 0x0C0C0000u;
-        r[j] = __builtin_amdgcn_perm(tr[1], tr[0], sel);
-      }
+    for (int i = 0; i < 4; i++) {
+      const uint32_t cw = *reinterpret_cast<const uint32_t*>(sm.codes + col_lds_row(16 * qq + 4 * a + i) * kColPitch + 4 * cg);
+      const uint32_t adj = (g - ((sw[a] >> (8 * i)) & 0xFFu)) & 0xFFu;
+      const u32x2 tr = *reinterpret_cast<const u32x2*>(&sm.table[adj][0]);
+      ev[i] = __builtin_amdgcn_perm(tr[1], tr[0], cw & 0x07070707u);
+      od[i] = __builtin_amdgcn_perm(tr[1], tr[0], (cw >> 4) & 0x07070707u);
     }
-    u32x4 oa, ob;
-#pragma unroll
-    for (int j4 = 0; j4 < 4; j4++) {
-      const uint32_t* rr = r + 4 * j4;
-      oa[j4] = __builtin_amdgcn_perm(rr[1], rr[0], 0x0C0C0400u) | (__builtin_amdgcn_perm(rr[3], rr[2], 0x0C0C0400u) << 16);
-      ob[j4] = __builtin_amdgcn_perm(rr[1], rr[0], 0x0C0C0501u) | (__builtin_amdgcn_perm(rr[3], rr[2], 0x0C0C0501u) << 16);
-    }
-    uint8_t* o = out + (bx * 256 + 2 * p) * M + row0 + 16 * qq;
-    __builtin_nontemporal_store(oa, reinterpret_cast<u32x4*>(o));
-    __builtin_nontemporal_store(ob, reinterpret_cast<u32x4*>(o + M));
+    // byte m of ev[i] / od[i] is element column 8cg + 2m / 2m + 1 of row 4a + i
+    const uint32_t e0 = __builtin_amdgcn_perm(ev[1], ev[0], 0x05010400u), e1 = __builtin_amdgcn_perm(ev[1], ev[0], 0x07030602u);
+    const uint32_t e2 = __builtin_amdgcn_perm(ev[3], ev[2], 0x05010400u), e3 = __builtin_amdgcn_perm(ev[3], ev[2], 0x07030602u);
+    const uint32_t o0 = __builtin_amdgcn_perm(od[1], od[0], 0x05010400u), o1 = __builtin_amdgcn_perm(od[1], od[0], 0x07030602u);
+    const uint32_t o2 = __builtin_amdgcn_perm(od[3], od[2], 0x05010400u), o3 = __builtin_amdgcn_perm(od[3], od[2], 0x07030602u);
+    col[0][a] = __builtin_amdgcn_perm(e2, e0, 0x05040100u);
+    col[2][a] = __builtin_amdgcn_perm(e2, e0, 0x07060302u);
+    col[4][a] = __builtin_amdgcn_perm(e3, e1, 0x05040100u);
+    col[6][a] = __builtin_amdgcn_perm(e3, e1, 0x07060302u);
+    col[1][a] = __builtin_amdgcn_perm(o2, o0, 0x05040100u);
+    col[3][a] = __builtin_amdgcn_perm(o2, o0, 0x07060302u);
+    col[5][a] = __builtin_amdgcn_perm(o3, o1, 0x05040100u);
+    col[7][a] = __builtin_amdgcn_perm(o3, o1, 0x07060302u);
   }
+  uint8_t* o = out + (bx * 256 + 8 * cg) * M + row0 + 16 * qq;
+#pragma unroll
+  for (int k = 0; k < 8; k++) __builtin_nontemporal_store(col[k], reinterpret_cast<u32x4*>(o + k * M));
 }
 
 hipError_t launch_mxfp4_to_fp8_col(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,

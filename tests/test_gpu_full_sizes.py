@@ -3,7 +3,8 @@ against the CPU oracle on the same inputs: the cfg3 dual layout (the
 columnwise half equal to the rowwise quantize of the transpose), the cfg5
 expert weights in one grouped launch, the cfg5 per-split row->col FP8 over the
 routed rows, the dense row->col FP8 at cfg4's shape, and the quantize at the
-cfg5 activation shapes (which take the one-pass kernel).
+cfg5 activation shapes (which take the one-pass kernel), and the transposed FP8
+requant at cfg4's shape.
 """
 import numpy as np
 import pytest
@@ -110,3 +111,23 @@ def test_quant_cfg5_activation_shapes(oracle, dev, K):
     eq, es = oracle.quant_mxfp4(xb)
     np.testing.assert_array_equal(bits_u8(s).reshape(-1), es)
     np.testing.assert_array_equal(bits_u8(q).reshape(-1), eq)
+
+
+def test_to_fp8_col_cfg4_full(oracle, dev):
+    """cfg4 shape: 4096 x 7168 MXFP4 -> FP8 transposed [7168, 4096] with the
+    fp32 scale rows."""
+    import omo
+    wl = _wl()
+    M, N = 4096, 7168
+    _say("to_fp8_col cfg4", M, N)
+    xb = bits_u16(wl.activations_with_outliers(M, N, seed=45, device="cpu")).reshape(-1)
+    q, s = oracle.quant_mxfp4(xb)
+    q, s = q.reshape(M, N // 2), s.reshape(M, N // 32)
+    out = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=dev)
+    outs = torch.empty((M // 128, N), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4ToFp8_col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, 128, 1e-10,
+                                     -6.0, 6.0, False)
+    torch.cuda.synchronize()
+    eo, es = oracle.mxfp4_to_fp8_col(q, s, eps=1e-10)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
