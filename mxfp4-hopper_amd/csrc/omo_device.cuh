@@ -111,15 +111,20 @@ __device__ __forceinline__ uint32_t e2m1_from_f32_ref(float q) {
   return ((sign >> 28) | r) & 0xFu;
 }
 
-// cvt_pk_f32_fp4<0>(src, scale, &lo, &hi): the two E2M1 nibbles of byte 0
-// of `src` times `scale`, as two fp32 values (exact for scale 2^k). Only
-// byte 0 is provided: it is the form the parity tests cover.
+// cvt_pk_f32_fp4<B>(src, scale, &lo, &hi): the two E2M1 nibbles of byte B
+// of `src` (low nibble -> lo) times `scale`, as two fp32 values (exact for
+// scale 2^k). Byte 0 is written as the bare instruction; bytes 1..3 use the
+// compiler builtin, which encodes the byte in op_sel.
 template <int B>
 __device__ __forceinline__ void cvt_pk_f32_fp4(uint32_t src, float scale, float* lo, float* hi) {
-  static_assert(B == 0, "only byte 0 of the source is supported");
+  static_assert(B >= 0 && B < 4, "byte select 0..3");
   typedef float f32x2_t __attribute__((ext_vector_type(2)));
   f32x2_t r;
-  asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2" : "=v"(r) : "v"(src), "v"(scale));
+  if constexpr (B == 0) {
+    asm("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2" : "=v"(r) : "v"(src), "v"(scale));
+  } else {
+    r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, scale, B);
+  }
   *lo = r[0];
   *hi = r[1];
 }

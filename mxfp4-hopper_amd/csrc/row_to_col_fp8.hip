@@ -374,6 +374,185 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_kernel(const uint8_
   }
 }
 
+// Dense kernel for whole aligned tiles of 128 rows x 256 element columns
+// (M % 128 == 0, N % 256 == 0, 16 B aligned codes and output, 8 B aligned
+// scales): one 256-thread block per tile, every block resident at once on
+// the shapes of the benchmark (896 tiles at 4096 x 7168). Lane t owns code
+// bytes 4c .. 4c+3 (element columns 8c .. 8c+7, one MX column), c = t / 8,
+// and rows 16q .. 16q+15, q = t % 8: per row it reads one code dword from
+// LDS (instead of one byte per two element columns), the 8 lanes of a code
+// dword reduce its 8 column maxima with DPP, lane q divides for column 8c + q
+// only (its scale-row entry and multiplier; the group reads the multipliers
+// back with ds_bpermute), and the 8 lanes write each of the 8 columns' 128
+// rows as one full 128 B line per store instruction. The arithmetic per
+// element and the fast-path conditions are those of rc_tile.
+constexpr int kWideCols = 256;
+constexpr int kWidePitch = 128 + 32;  // 16 B aligned LDS rows; 40 dwords keep a wave's row reads on distinct banks
+
+struct WideSmem {
+  uint8_t codes[kTile * kWidePitch];
+  uint32_t fscales[8][kTile];  // s << 23, [MX column of the tile][row]
+  uint8_t scales[8][kTile];
+};
+
+// Columns 2b, 2b+1 of the lane (the nibbles of code byte b) for its 16 rows.
+template <int B>
+__device__ __forceinline__ void wide_pair_fast(const uint32_t (&cw)[16], const float (&sc)[16], float m0, float m1,
+                                               u32x4& w0, u32x4& w1) {
+#pragma unroll
+  for (int j4 = 0; j4 < 4; j4++) {
+    float x[4], y[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      float v0, v1;
+      cvt_pk_f32_fp4<B>(cw[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
+      x[k] = v0 * m0;
+      y[k] = v1 * m1;
+    }
+    w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
+    w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+  }
+}
+
+// The column-maximum pass converts with volatile asm, so the compiler does not
+// keep its 128 values per lane alive for the output pass (which converts
+// again) and spill them.
+template <int B>
+__device__ __forceinline__ void cvt_pk_f32_fp4_once(uint32_t src, float scale, float* lo, float* hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  f32x2_t r;
+  if constexpr (B == 0) asm volatile("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2" : "=v"(r) : "v"(src), "v"(scale));
+  if constexpr (B == 1) asm volatile("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[1,0,0]" : "=v"(r) : "v"(src), "v"(scale));
+  if constexpr (B == 2) asm volatile("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[0,1,0]" : "=v"(r) : "v"(src), "v"(scale));
+  if constexpr (B == 3) asm volatile("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2 op_sel:[1,1,0]" : "=v"(r) : "v"(src), "v"(scale));
+  *lo = r[0];
+  *hi = r[1];
+}
+
+template <int B>
+__device__ __forceinline__ void wide_amax_fast(const uint32_t (&cw)[16], const float (&sc)[16], float (&a)[8]) {
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    float v0, v1;
+    cvt_pk_f32_fp4_once<B>(cw[j], sc[j], &v0, &v1);
+    a[2 * B] = fmaxf(a[2 * B], fabsf(v0));
+    a[2 * B + 1] = fmaxf(a[2 * B + 1], fabsf(v1));
+  }
+}
+
+__global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8_t* __restrict__ q,
+                                                                  const uint8_t* __restrict__ s,
+                                                                  uint8_t* __restrict__ out,
+                                                                  float* __restrict__ out_s, int64_t M, int64_t N,
+                                                                  float eps) {
+  __shared__ WideSmem sm;
+  const int t = threadIdx.x;
+  const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)(N / kWideCols);
+  const int64_t bn = L % gx, bm = L / gx;
+  const int64_t row0 = bm * kTile, col0 = bn * kWideCols;
+  // ---- stage codes (1024 chunks of 16 B, 8 rows x 128 B per wave load) and scales
+  u32x4 cv[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
+    cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
+  }
+  u32x2 sv = {0u, 0u};
+  if (t < kTile) sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
+    *reinterpret_cast<u32x4*>(sm.codes + lds_row(r) * kWidePitch + c16 * 16) = cv[k];
+  }
+  if (t < kTile) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const uint32_t b = (sv[c >> 2] >> (8 * (c & 3))) & 0xFFu;
+      sm.scales[c][t] = (uint8_t)b;
+      sm.fscales[c][t] = b << 23;
+    }
+  }
+  __syncthreads();
+  const int qq = t & 7, cg = t >> 3, mx = cg >> 2;
+  const u32x4 sw = *reinterpret_cast<const u32x4*>(&sm.scales[mx][16 * qq]);
+  uint32_t cw[16];
+  float sc[16];
+#pragma unroll
+  for (int j4 = 0; j4 < 4; j4++) {
+    const u32x4 f = *reinterpret_cast<const u32x4*>(&sm.fscales[mx][16 * qq + 4 * j4]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) sc[4 * j4 + k] = __uint_as_float(f[k]);
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j++) cw[j] = *reinterpret_cast<const uint32_t*>(sm.codes + lds_row(16 * qq + j) * kWidePitch + 4 * cg);
+  const bool fast = bytes_in_1_252(sw[0]) && bytes_in_1_252(sw[1]) && bytes_in_1_252(sw[2]) && bytes_in_1_252(sw[3]);
+  float a[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) a[e] = eps;
+  if (fast) {
+    wide_amax_fast<0>(cw, sc, a);
+    wide_amax_fast<1>(cw, sc, a);
+    wide_amax_fast<2>(cw, sc, a);
+    wide_amax_fast<3>(cw, sc, a);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const float s16 = bf16_to_f32(((sw[j >> 2] >> (8 * (j & 3))) & 0xFFu) << 7);
+#pragma unroll
+      for (int e = 0; e < 8; e++) a[e] = fmaxf(a[e], fabsf(bf16_to_f32(e2m1_to_bf16_bits((cw[j] >> (4 * e)) & 0xFu)) * s16));
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) a[e] = oct_fmax(a[e]);
+  // lane q: column 8c + q's scale-row entry amax / 448 and multiplier
+  // 448 / amax (0 when amax <= 1e-9)
+  float ae = a[0];
+#pragma unroll
+  for (int e = 1; e < 8; e++) ae = qq == e ? a[e] : ae;
+  float mown = 448.0f / ae;
+  if (!(ae > 1e-9f)) mown = 0.0f;
+  __builtin_nontemporal_store(ae / 448.0f, out_s + bm * N + col0 + 8 * cg + qq);
+  const int base = (t & 63) & ~7;
+  float m[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) m[e] = lane_value(mown, base + e);
+  uint8_t* o = out + (col0 + 8 * cg) * M + row0 + 16 * qq;
+  if (fast) {
+    // |v * m| <= 448 (1 + 2^-23) with |v| <= amax and m = fl(448 / amax):
+    // E4M3 RNE gives the clamped value without the clamp
+    u32x4 w0, w1;
+    wide_pair_fast<0>(cw, sc, m[0], m[1], w0, w1);
+    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o));
+    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + M));
+    wide_pair_fast<1>(cw, sc, m[2], m[3], w0, w1);
+    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o + 2 * M));
+    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + 3 * M));
+    wide_pair_fast<2>(cw, sc, m[4], m[5], w0, w1);
+    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o + 4 * M));
+    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + 5 * M));
+    wide_pair_fast<3>(cw, sc, m[6], m[7], w0, w1);
+    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o + 6 * M));
+    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + 7 * M));
+  } else {
+#pragma unroll 1
+    for (int e = 0; e < 8; e++) {
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 16; j += 2) {
+        float x[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const float s16 = bf16_to_f32(((sw[(j + h) >> 2] >> (8 * ((j + h) & 3))) & 0xFFu) << 7);
+          const float v = bf16_to_f32(e2m1_to_bf16_bits((cw[j + h] >> (4 * e)) & 0xFu)) * s16;
+          x[h] = fminf(fmaxf(v * m[e], -448.0f), 448.0f);
+        }
+        w[j >> 2] |= fp8x2_from_f32(x[0], x[1]) << (8 * (j & 3));
+      }
+      __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4*>(o + e * M));
+    }
+  }
+}
+
 // A split's output column c is a run of len bytes at off*N + c*len, so a
 // tile's 128-row piece of a column starts at an arbitrary byte alignment.
 // Each lane stores its 16 bytes of a column at their exact place: one 16 B
@@ -414,6 +593,12 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
   const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
   const bool vout = (M % 16 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
   const bool full = vin && vs && vout && (M % kTile == 0);
+  if (full && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
+    hipLaunchKernelGGL(row_to_fp8_col_wide_kernel, dim3((unsigned)((M / kTile) * (N / kWideCols))), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
+                       M, N, eps);
+    return hipGetLastError();
+  }
   const int64_t tiles_m = (M + kTile - 1) / kTile, tiles = tiles_m * ((N + kTile - 1) / kTile);
   // one wave of resident blocks: two 512-thread blocks per CU at this
   // kernel's register use (4 waves per SIMD)

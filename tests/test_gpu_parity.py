@@ -372,7 +372,10 @@ def payload_from_normal(M, K, seed, std=1.0):
     return q.reshape(M, K // 2), s.reshape(M, K // 32)
 
 
-@pytest.mark.parametrize("M,N,seed", [(128, 128, 1), (300, 7168, 2), (1, 64, 3), (129, 4096, 4), (1000, 2048, 5)])
+# (128, 128) takes the 128-column whole-tile kernel; (256, 256), (512, 7168),
+# (1024, 2048) and (128, 768) the 256-column one; the others ragged tiles.
+@pytest.mark.parametrize("M,N,seed", [(128, 128, 1), (300, 7168, 2), (1, 64, 3), (129, 4096, 4), (1000, 2048, 5),
+                                      (256, 256, 6), (512, 7168, 7), (1024, 2048, 8), (128, 768, 9)])
 def test_row_to_fp8_col_dense(oracle, dev, M, N, seed):
     _say("row_to_fp8_col", M, N)
     from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4RowToBf16ToFp8Col_wrapper
@@ -381,6 +384,22 @@ def test_row_to_fp8_col_dense(oracle, dev, M, N, seed):
     torch.cuda.synchronize()
     eo, es = oracle.row_to_fp8_col(q, s)
     assert out.shape == (N, M) and outs.shape == ((M + 127) // 128, N)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,eps", [(256, 512, 1e3), (300, 640, 1e3), (256, 512, 3.0)])
+def test_row_to_fp8_col_dense_eps(oracle, dev, M, N, eps):
+    """eps above (1e3) or among (3.0) the column maxima: the maximum seeded
+    with eps, on whole tiles and ragged ones."""
+    _say("row_to_fp8_col eps", M, N, eps)
+    omo = _omo()
+    q, s = payload_from_normal(M, N, 11)
+    out = torch.empty((N, M), dtype=FP8, device=dev)
+    outs = torch.empty(((M + 127) // 128, N), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, eps)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s, eps=eps)
     np.testing.assert_array_equal(bits_u8(out), eo)
     np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
 
