@@ -154,6 +154,25 @@ __device__ __forceinline__ float lane_value(float v, int src) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
 }
 
+// compute_te_pow2_scale (per_token_Mxfp4RowToBf16ToFp8Col_msplit.cu:23-43)
+// with FP8_E4M3_MAX = 448: multiplier 1/2^k and stored scale 2^k, 2^k the
+// smallest power of two at or above fl(amax / 448); 1 and 1 for amax <= eps.
+__device__ __forceinline__ void te_pow2_scale(float a, float eps, float* mult, float* inv) {
+  if (a <= eps) {
+    *mult = 1.0f;
+    *inv = 1.0f;
+    return;
+  }
+  const uint32_t b = __float_as_uint(a / 448.0f);
+  uint32_t e = (b >> 23) & 0xFFu;
+  if (b & 0x7FFFFFu) e += 1u;
+  *inv = __uint_as_float(e << 23);  // 2^(e-127); 0 for e == 0, inf for e == 255
+  if (e == 0u) *mult = __builtin_inff();
+  else if (e >= 255u) *mult = 0.0f;
+  else if (e == 254u) *mult = __uint_as_float(0x00400000u);  // 2^-127, subnormal
+  else *mult = exp2i(127 - (int)e);
+}
+
 // Column scale factors from the column amax. Every lane of an 8-lane column
 // group holds a0, a1 (the amax of columns 2p, 2p+1); lanes q = 0..3 of the
 // group each compute one of the four results and the group reads them back,
@@ -165,20 +184,7 @@ __device__ __forceinline__ void rc_factors(float a0, float a1, float eps, float*
   const float a = (qq & 1) ? a1 : a0;
   float mult, inv;
   if (MSPLIT) {
-    // compute_te_pow2_scale with FP8_E4M3_MAX = 448: multiplier 1/2^k, stored 2^k
-    if (a <= eps) {
-      mult = 1.0f;
-      inv = 1.0f;
-    } else {
-      const uint32_t b = __float_as_uint(a / 448.0f);
-      uint32_t e = (b >> 23) & 0xFFu;
-      if (b & 0x7FFFFFu) e += 1u;
-      inv = __uint_as_float(e << 23);  // 2^(e-127); 0 for e == 0, inf for e == 255
-      if (e == 0u) mult = __builtin_inff();
-      else if (e >= 255u) mult = 0.0f;
-      else if (e == 254u) mult = __uint_as_float(0x00400000u);  // 2^-127, subnormal
-      else mult = exp2i(127 - (int)e);
-    }
+    te_pow2_scale(a, eps, &mult, &inv);
     *m0 = lane_value(mult, base);
     *m1 = lane_value(mult, base + 1);
     *inv0 = lane_value(inv, base);
@@ -374,18 +380,18 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_kernel(const uint8_
   }
 }
 
-// Dense kernel for whole aligned tiles of 128 rows x 256 element columns
-// (M % 128 == 0, N % 256 == 0, 16 B aligned codes and output, 8 B aligned
-// scales): one 256-thread block per tile, every block resident at once on
-// the shapes of the benchmark (896 tiles at 4096 x 7168). Lane t owns code
+// Tiles of 128 rows x 256 element columns (N % 256 == 0, 16 B aligned codes,
+// 8 B aligned scales), one 256-thread workgroup per tile. Lane t owns code
 // bytes 4c .. 4c+3 (element columns 8c .. 8c+7, one MX column), c = t / 8,
 // and rows 16q .. 16q+15, q = t % 8: per row it reads one code dword from
 // LDS (instead of one byte per two element columns), the 8 lanes of a code
-// dword reduce its 8 column maxima with DPP, lane q divides for column 8c + q
-// only (its scale-row entry and multiplier; the group reads the multipliers
-// back with ds_bpermute), and the 8 lanes write each of the 8 columns' 128
-// rows as one full 128 B line per store instruction. The arithmetic per
-// element and the fast-path conditions are those of rc_tile.
+// dword reduce its 8 column maxima with DPP, lane q computes column 8c + q's
+// factors only (its scale-row entry and multiplier; the group reads the
+// multipliers back with ds_bpermute), and the 8 lanes write each of the 8
+// columns' 128 rows as eight 16 B pieces. The arithmetic per element and the
+// fast-path conditions are those of rc_tile. Used by the dense kernel on
+// whole aligned tensors (every workgroup resident at once on the benchmark
+// shapes: 896 tiles at 4096 x 7168) and by the per-split kernel.
 constexpr int kWideCols = 256;
 constexpr int kWidePitch = 128 + 32;  // 16 B aligned LDS rows; 40 dwords keep a wave's row reads on distinct banks
 
@@ -394,25 +400,6 @@ struct WideSmem {
   uint32_t fscales[8][kTile];  // s << 23, [MX column of the tile][row]
   uint8_t scales[8][kTile];
 };
-
-// Columns 2b, 2b+1 of the lane (the nibbles of code byte b) for its 16 rows.
-template <int B>
-__device__ __forceinline__ void wide_pair_fast(const uint32_t (&cw)[16], const float (&sc)[16], float m0, float m1,
-                                               u32x4& w0, u32x4& w1) {
-#pragma unroll
-  for (int j4 = 0; j4 < 4; j4++) {
-    float x[4], y[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      float v0, v1;
-      cvt_pk_f32_fp4<B>(cw[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
-      x[k] = v0 * m0;
-      y[k] = v1 * m1;
-    }
-    w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
-    w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
-  }
-}
 
 // The column-maximum pass converts with volatile asm, so the compiler does not
 // keep its 128 values per lane alive for the output pass (which converts
@@ -440,25 +427,49 @@ __device__ __forceinline__ void wide_amax_fast(const uint32_t (&cw)[16], const f
   }
 }
 
-__global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8_t* __restrict__ q,
-                                                                  const uint8_t* __restrict__ s,
-                                                                  uint8_t* __restrict__ out,
-                                                                  float* __restrict__ out_s, int64_t M, int64_t N,
-                                                                  float eps) {
-  __shared__ WideSmem sm;
+// Columns 2b, 2b+1 of the lane (the nibbles of code byte b) for its 16 rows.
+template <int B, bool CLAMP>
+__device__ __forceinline__ void wide_pair_fast(const uint32_t (&cw)[16], const float (&sc)[16], float m0, float m1,
+                                               u32x4& w0, u32x4& w1) {
+#pragma unroll
+  for (int j4 = 0; j4 < 4; j4++) {
+    float x[4], y[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      float v0, v1;
+      cvt_pk_f32_fp4<B>(cw[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
+      x[k] = CLAMP ? __builtin_amdgcn_fmed3f(v0 * m0, -448.0f, 448.0f) : v0 * m0;
+      y[k] = CLAMP ? __builtin_amdgcn_fmed3f(v1 * m1, -448.0f, 448.0f) : v1 * m1;
+    }
+    w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
+    w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+  }
+}
+
+// One tile: code rows row0 .. row0 + rows_valid - 1 (the others read as
+// codes 0 with scale 127, i.e. exact zeros), element columns col0 .. col0 +
+// 255. Element column col0 + e, tile row r is written at obase + e * cstride
+// + r; the scale-row entry of column col0 + e at out_s_row[e]. Dense
+// (MSPLIT false): rows_valid == 128, amax seeded with eps, factors 448 / amax
+// and amax / 448, 16 B aligned non-temporal stores. Per split: amax seeded
+// with 0, te_pow2_scale factors, stores at any alignment.
+template <bool MSPLIT>
+__device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                          int64_t N, int64_t row0, int rows_valid, int64_t col0, float eps,
+                                          float* __restrict__ out_s_row, uint8_t* __restrict__ obase, int64_t cstride) {
   const int t = threadIdx.x;
-  const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)(N / kWideCols);
-  const int64_t bn = L % gx, bm = L / gx;
-  const int64_t row0 = bm * kTile, col0 = bn * kWideCols;
   // ---- stage codes (1024 chunks of 16 B, 8 rows x 128 B per wave load) and scales
   u32x4 cv[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
-    cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
+    cv[k] = u32x4{0u, 0u, 0u, 0u};
+    if (!MSPLIT || r < rows_valid)
+      cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
   }
-  u32x2 sv = {0u, 0u};
-  if (t < kTile) sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
+  u32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
+  if (t < kTile && (!MSPLIT || t < rows_valid))
+    sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
@@ -488,7 +499,7 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8
   const bool fast = bytes_in_1_252(sw[0]) && bytes_in_1_252(sw[1]) && bytes_in_1_252(sw[2]) && bytes_in_1_252(sw[3]);
   float a[8];
 #pragma unroll
-  for (int e = 0; e < 8; e++) a[e] = eps;
+  for (int e = 0; e < 8; e++) a[e] = MSPLIT ? 0.0f : eps;
   if (fast) {
     wide_amax_fast<0>(cw, sc, a);
     wide_amax_fast<1>(cw, sc, a);
@@ -504,35 +515,68 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8
   }
 #pragma unroll
   for (int e = 0; e < 8; e++) a[e] = oct_fmax(a[e]);
-  // lane q: column 8c + q's scale-row entry amax / 448 and multiplier
-  // 448 / amax (0 when amax <= 1e-9)
   float ae = a[0];
 #pragma unroll
   for (int e = 1; e < 8; e++) ae = qq == e ? a[e] : ae;
-  float mown = 448.0f / ae;
-  if (!(ae > 1e-9f)) mown = 0.0f;
-  __builtin_nontemporal_store(ae / 448.0f, out_s + bm * N + col0 + 8 * cg + qq);
+  float mown, iown;
+  if (MSPLIT) {
+    te_pow2_scale(ae, eps, &mown, &iown);
+  } else {
+    // 448 / amax (0 when amax <= 1e-9) and amax / 448
+    mown = 448.0f / ae;
+    if (!(ae > 1e-9f)) mown = 0.0f;
+    iown = ae / 448.0f;
+  }
+  __builtin_nontemporal_store(iown, out_s_row + 8 * cg + qq);
   const int base = (t & 63) & ~7;
   float m[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) m[e] = lane_value(mown, base + e);
-  uint8_t* o = out + (col0 + 8 * cg) * M + row0 + 16 * qq;
-  if (fast) {
-    // |v * m| <= 448 (1 + 2^-23) with |v| <= amax and m = fl(448 / amax):
-    // E4M3 RNE gives the clamped value without the clamp
+  // The clamp to +-448 is left out where it changes no byte, as in rc_tile:
+  // always for the dense kernel; per split where every column has amax > eps
+  // or amax <= 448 (and finite multipliers).
+  bool finite_m = true, no_clamp = true;
+  if (MSPLIT) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      finite_m = finite_m && m[e] < __builtin_inff();
+      no_clamp = no_clamp && (a[e] > eps || a[e] <= 448.0f);
+    }
+  }
+  uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
+  auto put = [&](int e, const u32x4& w) {
+    if (MSPLIT) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
+    else __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(o + e * cstride));
+  };
+  if (fast && finite_m) {
     u32x4 w0, w1;
-    wide_pair_fast<0>(cw, sc, m[0], m[1], w0, w1);
-    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o));
-    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + M));
-    wide_pair_fast<1>(cw, sc, m[2], m[3], w0, w1);
-    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o + 2 * M));
-    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + 3 * M));
-    wide_pair_fast<2>(cw, sc, m[4], m[5], w0, w1);
-    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o + 4 * M));
-    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + 5 * M));
-    wide_pair_fast<3>(cw, sc, m[6], m[7], w0, w1);
-    __builtin_nontemporal_store(w0, reinterpret_cast<u32x4*>(o + 6 * M));
-    __builtin_nontemporal_store(w1, reinterpret_cast<u32x4*>(o + 7 * M));
+    if (no_clamp) {
+      wide_pair_fast<0, false>(cw, sc, m[0], m[1], w0, w1);
+      put(0, w0);
+      put(1, w1);
+      wide_pair_fast<1, false>(cw, sc, m[2], m[3], w0, w1);
+      put(2, w0);
+      put(3, w1);
+      wide_pair_fast<2, false>(cw, sc, m[4], m[5], w0, w1);
+      put(4, w0);
+      put(5, w1);
+      wide_pair_fast<3, false>(cw, sc, m[6], m[7], w0, w1);
+      put(6, w0);
+      put(7, w1);
+    } else {
+      wide_pair_fast<0, true>(cw, sc, m[0], m[1], w0, w1);
+      put(0, w0);
+      put(1, w1);
+      wide_pair_fast<1, true>(cw, sc, m[2], m[3], w0, w1);
+      put(2, w0);
+      put(3, w1);
+      wide_pair_fast<2, true>(cw, sc, m[4], m[5], w0, w1);
+      put(4, w0);
+      put(5, w1);
+      wide_pair_fast<3, true>(cw, sc, m[6], m[7], w0, w1);
+      put(6, w0);
+      put(7, w1);
+    }
   } else {
 #pragma unroll 1
     for (int e = 0; e < 8; e++) {
@@ -548,9 +592,43 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8
         }
         w[j >> 2] |= fp8x2_from_f32(x[0], x[1]) << (8 * (j & 3));
       }
-      __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4*>(o + e * M));
+      put(e, u32x4{w[0], w[1], w[2], w[3]});
     }
   }
+}
+
+// Dense: whole aligned tensors (M % 128 == 0, N % 256 == 0, 16 B aligned
+// output), tile (bm, bn) = blockIdx renumbered per XCD, bn fastest.
+__global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8_t* __restrict__ q,
+                                                                     const uint8_t* __restrict__ s,
+                                                                     uint8_t* __restrict__ out,
+                                                                     float* __restrict__ out_s, int64_t M, int64_t N,
+                                                                     float eps) {
+  __shared__ WideSmem sm;
+  const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)(N / kWideCols);
+  const int64_t bn = L % gx, bm = L / gx;
+  const int64_t row0 = bm * kTile, col0 = bn * kWideCols;
+  wide_tile<false>(sm, q, s, N, row0, kTile, col0, eps, out_s + bm * N + col0, out + col0 * M + row0, M);
+}
+
+// Per split, N % 256 == 0: workgroup (split, bm, bn) as in
+// row_to_fp8_col_msplit_kernel.
+__global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_wide_kernel(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
+    const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
+    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps) {
+  __shared__ WideSmem sm;
+  const int64_t split = blockIdx.x, bm = blockIdx.y, bn = blockIdx.z;
+  const int64_t len = lens[split];
+  if (bm * kTile >= len) return;
+  const int64_t start = offs[split], sstart = soffs[split];
+  // Metadata arrives on the device; tiles whose rows or scale rows fall
+  // outside the buffers are skipped rather than written out of bounds.
+  if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
+  const int64_t row0 = start + bm * kTile, col0 = bn * kWideCols;
+  const int rows_valid = (int)(len - bm * kTile < kTile ? len - bm * kTile : kTile);
+  wide_tile<true>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + (sstart + bm) * N + col0,
+                  out + start * N + col0 * len + bm * kTile, len);
 }
 
 // A split's output column c is a run of len bytes at off*N + c*len, so a
@@ -619,6 +697,13 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   if (nsplits == 0 || max_split_len <= 0 || N == 0) return hipSuccess;
   const bool vin = (N % 32 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
   const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
+  if (vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
+    dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)(N / kWideCols));
+    hipLaunchKernelGGL(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
+                       static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs,
+                       total_rows, N, out_s_rows, eps);
+    return hipGetLastError();
+  }
   dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)((N + kTile - 1) / kTile));
   hipLaunchKernelGGL(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
