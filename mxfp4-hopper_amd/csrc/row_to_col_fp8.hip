@@ -319,11 +319,34 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
 // tile) to dst[0 .. 16), stopping at rows_valid. dst may have any byte
 // alignment: the 16 B store is emitted as one global_store_dwordx4, which
 // the hardware splits when it is unaligned (checked at every offset 0..15).
+// A partial piece of n = 1..15 bytes is written as at most four stores of 8,
+// 4, 2 and 1 bytes (the bits of n, largest first), so each one's source
+// bytes start at a multiple of its size within the 16 (a loop of single
+// byte stores cost 4 us over cfg5's ragged splits).
 __device__ __forceinline__ void rc_store(uint8_t* __restrict__ dst, const u32x4& w, int r_base, int rows_valid) {
   if (r_base + 16 <= rows_valid) {
     __builtin_memcpy(dst, &w, 16);
-  } else {
-    for (int j = 0; j < 16 && r_base + j < rows_valid; j++) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+  } else if (r_base < rows_valid) {
+    const int n = rows_valid - r_base;
+    int pos = 0;
+    if (n & 8) {
+      const u32x2 h = {w[0], w[1]};
+      __builtin_memcpy(dst, &h, 8);
+      pos = 8;
+    }
+    const uint32_t wd = pos ? w[2] : w[0];  // dword holding byte pos
+    const uint32_t wn = pos ? w[3] : w[1];  // the next one
+    if (n & 4) {
+      __builtin_memcpy(dst + pos, &wd, 4);
+      pos += 4;
+    }
+    const uint32_t v = (n & 4) ? wn : wd;   // dword holding byte pos now
+    if (n & 2) {
+      const uint16_t h = (uint16_t)v;
+      __builtin_memcpy(dst + pos, &h, 2);
+      pos += 2;
+    }
+    if (n & 1) dst[pos] = (uint8_t)((n & 2) ? v >> 16 : v);
   }
 }
 
