@@ -478,10 +478,11 @@ def test_row_to_fp8_col_msplit(oracle, dev, splits, N):
 
 # Lengths 17i (i = 1..15) end a tile's column piece after every count 1..15
 # of bytes of a 16-row block, on the 256-column kernel (N = 256) and the
-# 128-column one (N = 384).
+# 128-column one (N = 384). Lengths that are multiples of 128 among ragged
+# ones (N = 512) mix line-aligned tiles (non-temporal stores) with the others.
 @pytest.mark.parametrize("splits,N", [([211, 97, 300, 5, 256, 130], 7168), ([2083, 17, 1965], 1024),
                                       ([129, 255, 383, 1, 16, 144], 384), ([17 * i for i in range(1, 16)], 256),
-                                      ([17 * i for i in range(1, 16)], 384)])
+                                      ([17 * i for i in range(1, 16)], 384), ([256, 100, 128, 0, 384, 17, 640], 512)])
 def test_row_to_fp8_col_msplit_every_byte(oracle, dev, splits, N):
     """Ragged splits (column runs at every byte alignment, pieces that end
     inside a 16 B block) into outputs pre-filled with a sentinel, so a byte
