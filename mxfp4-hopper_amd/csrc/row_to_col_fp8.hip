@@ -732,7 +732,13 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
   if (vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
     dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)(N / kWideCols));
-    hipLaunchKernelGGL(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
+    // Unused dynamic LDS caps residency at 4 workgroups per CU (6 by the
+    // kernel's own LDS and registers): fewer tiles' partial output lines wait
+    // in L2 at once. Ragged cfg5 splits: 49.6 us against 51.0, and 59.8 against
+    // 62.8 right after a 512 MB fill (dirty caches, as in a layer step).
+    const int per_wg = current_device_caps().lds_per_workgroup / 4 - 2560;
+    const size_t reserve = per_wg > (int)sizeof(WideSmem) ? (size_t)(per_wg - (int)sizeof(WideSmem)) : 0;
+    hipLaunchKernelGGL(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
                        static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs,
                        total_rows, N, out_s_rows, eps, (reinterpret_cast<uintptr_t>(out) & 127) == 0);
     return hipGetLastError();
