@@ -18,7 +18,11 @@
 // out_s = 1/scale at [(soff_i + tile) * N + c], q = v * scale, and the
 // split's output block [N, len_i] starts at off_i * N.
 //
-// One 512-thread block per tile. The tile's code bytes (128 rows x 64 B) and
+// Two tile shapes. Where N % 256 == 0 (with 16 B aligned codes and 8 B
+// aligned scales) tiles are 128 rows x 256 element columns, one 256-thread
+// workgroup each, a lane per code dword (wide_tile, below). Other shapes
+// take 128 x 128 tiles, one 512-thread block per tile, described here.
+// The tile's code bytes (128 rows x 64 B) and
 // scale bytes are staged in LDS. Lane t owns code-byte column p = t/8 (two
 // element columns) and the 16 rows of eighth q = t%8, so 8 adjacent lanes
 // hold a full tile column: the column amax is two quad_perm steps and one
