@@ -20,8 +20,8 @@
 //
 // Two tile shapes. Where N % 256 == 0 (with 16 B aligned codes and 8 B
 // aligned scales) tiles are 128 rows x 256 element columns, one 256-thread
-// workgroup each, a lane per code dword (wide_tile, below). Other shapes
-// take 128 x 128 tiles, one 512-thread block per tile, described here.
+// workgroup each, a lane per code dword (wide_tile, below), for any M. Other
+// shapes take 128 x 128 tiles, one 512-thread block per tile, described here.
 // The tile's code bytes (128 rows x 64 B) and
 // scale bytes are staged in LDS. Lane t owns code-byte column p = t/8 (two
 // element columns) and the 16 rows of eighth q = t%8, so 8 adjacent lanes
@@ -477,13 +477,14 @@ __device__ __forceinline__ void wide_pair_fast(const uint32_t (&cw)[16], const f
 // codes 0 with scale 127, i.e. exact zeros), element columns col0 .. col0 +
 // 255. Element column col0 + e, tile row r is written at obase + e * cstride
 // + r; the scale-row entry of column col0 + e at out_s_row[e]. Dense
-// (MSPLIT false): rows_valid == 128, amax seeded with eps, factors 448 / amax
-// and amax / 448, 16 B aligned non-temporal stores. Per split: amax seeded
-// with 0, te_pow2_scale factors; with line_nt (every column piece of the
-// tile is one whole 128 B line) non-temporal stores, otherwise ordinary
-// stores at any alignment, whose partial lines (shared with the neighbouring
-// tiles of the column) are completed in L2.
-template <bool MSPLIT>
+// (MSPLIT false): amax seeded with eps, factors 448 / amax and amax / 448.
+// Per split: amax seeded with 0, te_pow2_scale factors. RAGGED: rows_valid
+// may be below 128 and the output pieces may have any alignment; stores are
+// then ordinary stores at the exact place, whose partial lines (shared with
+// the neighbouring tiles of the column) are completed in L2, unless line_nt
+// says every column piece of the tile is one whole 128 B line. Not RAGGED:
+// rows_valid == 128 and 16 B aligned non-temporal stores.
+template <bool MSPLIT, bool RAGGED>
 __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
                                           int64_t N, int64_t row0, int rows_valid, int64_t col0, float eps,
                                           float* __restrict__ out_s_row, uint8_t* __restrict__ obase, int64_t cstride,
@@ -495,11 +496,11 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   for (int k = 0; k < 4; k++) {
     const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
     cv[k] = u32x4{0u, 0u, 0u, 0u};
-    if (!MSPLIT || r < rows_valid)
+    if (!RAGGED || r < rows_valid)
       cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
   }
   u32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
-  if (t < kTile && (!MSPLIT || t < rows_valid))
+  if (t < kTile && (!RAGGED || t < rows_valid))
     sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -576,7 +577,7 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   }
   uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
   auto put = [&](int e, const u32x4& w) {
-    if (MSPLIT && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
+    if (RAGGED && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
     else __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(o + e * cstride));
   };
   if (fast && finite_m) {
@@ -628,8 +629,10 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   }
 }
 
-// Dense: whole aligned tensors (M % 128 == 0, N % 256 == 0, 16 B aligned
-// output), tile (bm, bn) = blockIdx renumbered per XCD, bn fastest.
+// Dense, N % 256 == 0, tile (bm, bn) = blockIdx renumbered per XCD, bn
+// fastest. Not RAGGED: whole aligned tiles (M % 128 == 0, 16 B aligned
+// output). RAGGED: any M, any output alignment (the last row tile partial).
+template <bool RAGGED>
 __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8_t* __restrict__ q,
                                                                      const uint8_t* __restrict__ s,
                                                                      uint8_t* __restrict__ out,
@@ -639,7 +642,9 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8
   const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)(N / kWideCols);
   const int64_t bn = L % gx, bm = L / gx;
   const int64_t row0 = bm * kTile, col0 = bn * kWideCols;
-  wide_tile<false>(sm, q, s, N, row0, kTile, col0, eps, out_s + bm * N + col0, out + col0 * M + row0, M, true);
+  const int rows_valid = RAGGED ? (int)(M - row0 < kTile ? M - row0 : kTile) : kTile;
+  wide_tile<false, RAGGED>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + bm * N + col0, out + col0 * M + row0, M,
+                           false);
 }
 
 // Per split, N % 256 == 0: workgroup (split, bm, bn) as in
@@ -664,7 +669,7 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_wide_kernel(
   if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
   const int64_t row0 = start + bm * kTile, col0 = bn * kWideCols;
   const int rows_valid = (int)(len - bm * kTile < kTile ? len - bm * kTile : kTile);
-  wide_tile<true>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + (sstart + bm) * N + col0,
+  wide_tile<true, true>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + (sstart + bm) * N + col0,
                   out + start * N + col0 * len + bm * kTile, len, out_line && len % kTile == 0);
 }
 
@@ -708,10 +713,11 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
   const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
   const bool vout = (M % 16 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
   const bool full = vin && vs && vout && (M % kTile == 0);
-  if (full && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
-    hipLaunchKernelGGL(row_to_fp8_col_wide_kernel, dim3((unsigned)((M / kTile) * (N / kWideCols))), dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
-                       M, N, eps);
+  if (vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
+    const dim3 grid((unsigned)(((M + kTile - 1) / kTile) * (N / kWideCols)));
+    auto kernel = full ? row_to_fp8_col_wide_kernel<false> : row_to_fp8_col_wide_kernel<true>;
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s),
+                       static_cast<uint8_t*>(out), out_s, M, N, eps);
     return hipGetLastError();
   }
   const int64_t tiles_m = (M + kTile - 1) / kTile, tiles = tiles_m * ((N + kTile - 1) / kTile);

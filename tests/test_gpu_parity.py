@@ -372,8 +372,9 @@ def payload_from_normal(M, K, seed, std=1.0):
     return q.reshape(M, K // 2), s.reshape(M, K // 32)
 
 
-# (128, 128) takes the 128-column whole-tile kernel; (256, 256), (512, 7168),
-# (1024, 2048) and (128, 768) the 256-column one; the others ragged tiles.
+# (128, 128) takes the 128-column whole-tile kernel and (1, 64) its ragged
+# form; (256, 256), (512, 7168), (1024, 2048) and (128, 768) the 256-column
+# whole-tile kernel; (300, 7168), (129, 4096) and (1000, 2048) its ragged form.
 @pytest.mark.parametrize("M,N,seed", [(128, 128, 1), (300, 7168, 2), (1, 64, 3), (129, 4096, 4), (1000, 2048, 5),
                                       (256, 256, 6), (512, 7168, 7), (1024, 2048, 8), (128, 768, 9)])
 def test_row_to_fp8_col_dense(oracle, dev, M, N, seed):
@@ -384,6 +385,24 @@ def test_row_to_fp8_col_dense(oracle, dev, M, N, seed):
     torch.cuda.synchronize()
     eo, es = oracle.row_to_fp8_col(q, s)
     assert out.shape == (N, M) and outs.shape == ((M + 127) // 128, N)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N", [(1, 256), (17, 512), (300, 512), (4001, 2048), (4000, 7168)])
+def test_row_to_fp8_col_dense_ragged_sentinel(oracle, dev, M, N):
+    """Row counts that leave the last 128-row tile partial (and output
+    columns at any byte alignment for odd M), on the 256-column tiles, into
+    outputs pre-filled with a sentinel so that a byte the kernel fails to
+    write cannot pass."""
+    _say("row_to_fp8_col ragged sentinel", M, N)
+    omo = _omo()
+    q, s = payload_from_normal(M, N, M + 3)
+    out = torch.full((N, M), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    outs = torch.full(((M + 127) // 128, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s)
     np.testing.assert_array_equal(bits_u8(out), eo)
     np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
 
