@@ -473,61 +473,28 @@ __device__ __forceinline__ void wide_pair_fast(const uint32_t (&cw)[16], const f
   }
 }
 
-// One tile: code rows row0 .. row0 + rows_valid - 1 (the others read as
-// codes 0 with scale 127, i.e. exact zeros), element columns col0 .. col0 +
-// 255. Element column col0 + e, tile row r is written at obase + e * cstride
-// + r; the scale-row entry of column col0 + e at out_s_row[e]. Dense
-// (MSPLIT false): amax seeded with eps, factors 448 / amax and amax / 448.
-// Per split: amax seeded with 0, te_pow2_scale factors. RAGGED: rows_valid
-// may be below 128 and the output pieces may have any alignment; stores are
-// then ordinary stores at the exact place, whose partial lines (shared with
-// the neighbouring tiles of the column) are completed in L2, unless line_nt
-// says every column piece of the tile is one whole 128 B line. Not RAGGED:
-// rows_valid == 128 and 16 B aligned non-temporal stores.
-template <bool MSPLIT, bool RAGGED>
-__device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
-                                          int64_t N, int64_t row0, int rows_valid, int64_t col0, float eps,
-                                          float* __restrict__ out_s_row, uint8_t* __restrict__ obase, int64_t cstride,
-                                          bool line_nt) {
-  const int t = threadIdx.x;
-  // ---- stage codes (1024 chunks of 16 B, 8 rows x 128 B per wave load) and scales
-  u32x4 cv[4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
-    cv[k] = u32x4{0u, 0u, 0u, 0u};
-    if (!RAGGED || r < rows_valid)
-      cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
-  }
-  u32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
-  if (t < kTile && (!RAGGED || t < rows_valid))
-    sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
-    *reinterpret_cast<u32x4*>(sm.codes + lds_row(r) * kWidePitch + c16 * 16) = cv[k];
-  }
-  if (t < kTile) {
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-      const uint32_t b = (sv[c >> 2] >> (8 * (c & 3))) & 0xFFu;
-      sm.scales[c][t] = (uint8_t)b;
-      sm.fscales[c][t] = b << 23;
-    }
-  }
-  __syncthreads();
-  const int qq = t & 7, cg = t >> 3, mx = cg >> 2;
-  const u32x4 sw = *reinterpret_cast<const u32x4*>(&sm.scales[mx][16 * qq]);
+// Conversion of one staged wide tile: lane (cg, qq) converts element columns
+// 8cg .. 8cg+7 of tile rows 16qq .. 16qq+15 and hands column e's 16 bytes
+// (rows in order) to put(e, w). codes: the tile's first LDS code row (rows
+// permuted by lds_row, pitch bytes apart); scl / fscl: the 128 scale bytes
+// and 2^(s-127) patterns of the lane's MX column. The scale-row entry of
+// column 8cg + qq goes to out_s_lane when store_s. The 8 lanes of a code
+// dword must be 8 adjacent lanes of a wave.
+template <bool MSPLIT, typename Put>
+__device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, const uint8_t* scl, const uint32_t* fscl,
+                                             int cg, int qq, float eps, bool store_s, float* __restrict__ out_s_lane,
+                                             Put&& put) {
+  const u32x4 sw = *reinterpret_cast<const u32x4*>(scl + 16 * qq);
   uint32_t cw[16];
   float sc[16];
 #pragma unroll
   for (int j4 = 0; j4 < 4; j4++) {
-    const u32x4 f = *reinterpret_cast<const u32x4*>(&sm.fscales[mx][16 * qq + 4 * j4]);
+    const u32x4 f = *reinterpret_cast<const u32x4*>(fscl + 16 * qq + 4 * j4);
 #pragma unroll
     for (int k = 0; k < 4; k++) sc[4 * j4 + k] = __uint_as_float(f[k]);
   }
 #pragma unroll
-  for (int j = 0; j < 16; j++) cw[j] = *reinterpret_cast<const uint32_t*>(sm.codes + lds_row(16 * qq + j) * kWidePitch + 4 * cg);
+  for (int j = 0; j < 16; j++) cw[j] = *reinterpret_cast<const uint32_t*>(codes + lds_row(16 * qq + j) * pitch + 4 * cg);
   const bool fast = bytes_in_1_252(sw[0]) && bytes_in_1_252(sw[1]) && bytes_in_1_252(sw[2]) && bytes_in_1_252(sw[3]);
   float a[8];
 #pragma unroll
@@ -559,8 +526,8 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
     if (!(ae > 1e-9f)) mown = 0.0f;
     iown = ae / 448.0f;
   }
-  __builtin_nontemporal_store(iown, out_s_row + 8 * cg + qq);
-  const int base = (t & 63) & ~7;
+  if (store_s) __builtin_nontemporal_store(iown, out_s_lane);
+  const int base = (int)(threadIdx.x & 63) & ~7;
   float m[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) m[e] = lane_value(mown, base + e);
@@ -575,11 +542,6 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
       no_clamp = no_clamp && (a[e] > eps || a[e] <= 448.0f);
     }
   }
-  uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
-  auto put = [&](int e, const u32x4& w) {
-    if (RAGGED && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
-    else __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(o + e * cstride));
-  };
   if (fast && finite_m) {
     u32x4 w0, w1;
     if (no_clamp) {
@@ -627,6 +589,58 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
       put(e, u32x4{w[0], w[1], w[2], w[3]});
     }
   }
+}
+
+// One tile: code rows row0 .. row0 + rows_valid - 1 (the others read as
+// codes 0 with scale 127, i.e. exact zeros), element columns col0 .. col0 +
+// 255. Element column col0 + e, tile row r is written at obase + e * cstride
+// + r; the scale-row entry of column col0 + e at out_s_row[e]. Dense
+// (MSPLIT false): amax seeded with eps, factors 448 / amax and amax / 448.
+// Per split: amax seeded with 0, te_pow2_scale factors. RAGGED: rows_valid
+// may be below 128 and the output pieces may have any alignment; stores are
+// then ordinary stores at the exact place, whose partial lines (shared with
+// the neighbouring tiles of the column) are completed in L2, unless line_nt
+// says every column piece of the tile is one whole 128 B line. Not RAGGED:
+// rows_valid == 128 and 16 B aligned non-temporal stores.
+template <bool MSPLIT, bool RAGGED>
+__device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                          int64_t N, int64_t row0, int rows_valid, int64_t col0, float eps,
+                                          float* __restrict__ out_s_row, uint8_t* __restrict__ obase, int64_t cstride,
+                                          bool line_nt) {
+  const int t = threadIdx.x;
+  // ---- stage codes (1024 chunks of 16 B, 8 rows x 128 B per wave load) and scales
+  u32x4 cv[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
+    cv[k] = u32x4{0u, 0u, 0u, 0u};
+    if (!RAGGED || r < rows_valid)
+      cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
+  }
+  u32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
+  if (t < kTile && (!RAGGED || t < rows_valid))
+    sv = *reinterpret_cast<const u32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
+    *reinterpret_cast<u32x4*>(sm.codes + lds_row(r) * kWidePitch + c16 * 16) = cv[k];
+  }
+  if (t < kTile) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const uint32_t b = (sv[c >> 2] >> (8 * (c & 3))) & 0xFFu;
+      sm.scales[c][t] = (uint8_t)b;
+      sm.fscales[c][t] = b << 23;
+    }
+  }
+  __syncthreads();
+  const int qq = t & 7, cg = t >> 3, mx = cg >> 2;
+  uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
+  wide_convert<MSPLIT>(sm.codes, kWidePitch, sm.scales[mx], sm.fscales[mx], cg, qq, eps, true,
+                              out_s_row + 8 * cg + qq, [&](int e, const u32x4& w) {
+                                if (RAGGED && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
+                                else __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(o + e * cstride));
+                              });
 }
 
 // Dense, N % 256 == 0, tile (bm, bn) = blockIdx renumbered per XCD, bn
