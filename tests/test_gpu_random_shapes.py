@@ -19,6 +19,12 @@ ROWCOL_SHAPES = [(int(RNG.integers(1, 700)), 32 * int(RNG.integers(1, 50))) for 
 MSPLIT_CASES = [([int(v) for v in RNG.integers(0, 400, size=int(RNG.integers(1, 12)))], 128 * int(RNG.integers(1, 8)))
                 for _ in range(8)]
 QUANT_SHAPES = [(int(RNG.integers(1, 3000)), 32 * int(RNG.integers(1, 300))) for _ in range(8)]
+# row counts whole (multiple of 128) and ragged, N a multiple of 256 (the 256-column tiles)
+RNG_W = np.random.default_rng(20261202)
+ROWCOL_WIDE_SHAPES = [(int(v), 256 * int(RNG_W.integers(1, 12))) for v in
+                      list(128 * RNG_W.integers(1, 12, size=3)) + list(RNG_W.integers(1, 1500, size=5))]
+MSPLIT_WIDE_CASES = [([int(v) for v in RNG_W.integers(0, 700, size=int(RNG_W.integers(1, 10)))],
+                      256 * int(RNG_W.integers(1, 8))) for _ in range(5)]
 
 
 def _say(*a):
@@ -120,3 +126,37 @@ def test_quant_dequant_random(oracle, dev, M, K):
         omo.omo_per_token_Mxfp4ToBf16_dequant(q.view(-1), s.view(-1), y, unused, 32, 1e-10, -6.0, 6.0, False)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(bits_u16(y).reshape(-1), oracle.dequant_bf16(eq, es))
+
+
+@pytest.mark.parametrize("M,N", ROWCOL_WIDE_SHAPES)
+def test_row_to_fp8_col_wide_random(oracle, dev, M, N):
+    import omo
+    _say("row->col wide random", M, N)
+    q, s = _payload(M, N, M * 3 + N)
+    out = torch.full((N, M), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    outs = torch.full(((M + 127) // 128, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+@pytest.mark.parametrize("splits,N", MSPLIT_WIDE_CASES)
+def test_msplit_wide_random(oracle, dev, splits, N):
+    import omo
+    from omo_python_api.mxfp4_dequant import split_metadata
+    M = sum(splits)
+    _say("msplit wide random", splits, N)
+    if M == 0:
+        pytest.skip("all splits empty")
+    q, s = _payload(M, N, M % 997)
+    lens, offs, soffs, max_len, rows, srows = split_metadata(splits, dev)
+    out_q = torch.full((M * N,), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    out_s = torch.full((max(srows, 1), N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out_q,
+                                                    out_s, lens, offs, soffs, max_len, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(bits_u8(out_q), eo)
+    np.testing.assert_array_equal(out_s.cpu().numpy().view(np.uint32)[:srows], es.view(np.uint32))
