@@ -636,11 +636,11 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   __syncthreads();
   const int qq = t & 7, cg = t >> 3, mx = cg >> 2;
   uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
-  wide_convert<MSPLIT>(sm.codes, kWidePitch, sm.scales[mx], sm.fscales[mx], cg, qq, eps, true,
-                              out_s_row + 8 * cg + qq, [&](int e, const u32x4& w) {
-                                if (RAGGED && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
-                                else __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(o + e * cstride));
-                              });
+  wide_convert<MSPLIT>(sm.codes, kWidePitch, sm.scales[mx], sm.fscales[mx], cg, qq, eps, true, out_s_row + 8 * cg + qq,
+                       [&](int e, const u32x4& w) {
+                         if (RAGGED && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
+                         else __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(o + e * cstride));
+                       });
 }
 
 // Dense, N % 256 == 0, tile (bm, bn) = blockIdx renumbered per XCD, bn
