@@ -9,21 +9,43 @@
 // so the expert-parallel payload rows [codes | scales] are read in place.
 //
 // One wave per output row, 4 rows per 256-thread workgroup; each lane moves
-// V-sized pieces (16 B when every row start and row length allows it).
+// V-sized pieces (16 B when every row start and row length allows it), four
+// loads in flight before their stores. Source rows are read with ordinary
+// loads: a token routed to k experts is read k times, and the repeats then
+// come from cache. Code rows (whole 128 B lines at H % 256 == 0) are stored
+// non-temporally; scale rows (H/32 bytes, sharing lines with the next output
+// row) with ordinary stores, so their lines are completed in L2.
 #include "omo_device.cuh"
 #include "omo_internal.h"
 
 namespace omo_hip {
 
-template <typename V>
+template <typename V, bool NT_OUT>
 __device__ __forceinline__ void copy_row(const uint8_t* __restrict__ in, bool ok, uint8_t* __restrict__ out,
                                          int64_t bytes, int lane) {
+  constexpr int U = 4;
   const int64_t n = bytes / (int64_t)sizeof(V);
   const V* src = reinterpret_cast<const V*>(in);
   V* dst = reinterpret_cast<V*>(out);
   V zero;
   memset(&zero, 0, sizeof(V));
-  for (int64_t i = lane; i < n; i += 64) dst[i] = ok ? __builtin_nontemporal_load(src + i) : zero;
+  for (int64_t i0 = lane; i0 < n; i0 += 64 * U) {
+    V v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t i = i0 + 64 * u;
+      v[u] = zero;
+      if (ok && i < n) v[u] = src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t i = i0 + 64 * u;
+      if (i < n) {
+        if (NT_OUT) __builtin_nontemporal_store(v[u], dst + i);
+        else dst[i] = v[u];
+      }
+    }
+  }
 }
 
 template <typename V>
@@ -39,8 +61,8 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const uint8_t* __restr
   const int64_t sr = src[r];
   const bool ok = sr >= 0 && sr < n_src;
   const int64_t rr = ok ? sr : 0;
-  copy_row<V>(a + rr * a_stride, ok, out_a + r * a_bytes, a_bytes, lane);
-  copy_row<V>(b + rr * b_stride, ok, out_b + r * b_bytes, b_bytes, lane);
+  copy_row<V, true>(a + rr * a_stride, ok, out_a + r * a_bytes, a_bytes, lane);
+  copy_row<V, false>(b + rr * b_stride, ok, out_b + r * b_bytes, b_bytes, lane);
 }
 
 hipError_t launch_gather_rows(const void* a, int64_t a_stride, int64_t a_bytes, const void* b, int64_t b_stride,

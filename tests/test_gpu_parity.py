@@ -740,6 +740,32 @@ def test_payload_dequant_and_requant(oracle, dev, T, H, seed, spread):
 
 
 # ---------------------------------------------------------------- permutation
+def test_permute_rows_byte_pieces(dev):
+    """H = 96: 3-byte scale rows (and 51-byte payload rows) take the gather's
+    byte-wise copy; numpy indexing as the reference, zero padding rows."""
+    from omo_python_api.permutation import mxfp4_permute, payload_views
+    T, H, E, k, pad = 37, 96, 5, 2, 3
+    _say("permute byte pieces", T, H)
+    rng = np.random.default_rng(9)
+    q = rng.integers(0, 256, size=(T, H // 2), dtype=np.uint8)
+    s = rng.integers(100, 150, size=(T, H // 32), dtype=np.uint8)
+    rm = np.zeros((T, E), bool)
+    for t in range(T):
+        rm[t, rng.choice(E, k, replace=False)] = True
+    e_idx, t_idx = np.nonzero(rm.T)
+    n = t_idx.size
+    exp_q = np.zeros((n + pad, H // 2), np.uint8)
+    exp_s = np.zeros((n + pad, H // 32), np.uint8)
+    exp_q[:n], exp_s[:n] = q[t_idx], s[t_idx]
+    rmt = torch.from_numpy(rm).to(dev)
+    cq, cs, _, _, _ = mxfp4_permute(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), rmt, None, n + pad)
+    payload = torch.from_numpy(np.ascontiguousarray(np.concatenate([q, s], axis=1))).to(dev)
+    cq2, cs2, _, _, _ = mxfp4_permute(*payload_views(payload), rmt, None, n + pad)
+    torch.cuda.synchronize()
+    for a, b in ((cq, exp_q), (cs, exp_s), (cq2, exp_q), (cs2, exp_s)):
+        np.testing.assert_array_equal(bits_u8(a), b)
+
+
 @pytest.mark.parametrize("T,H,E,k,pad,seed", [(300, 7168, 8, 2, 0, 1), (64, 256, 4, 1, 7, 2), (5, 128, 3, 3, 0, 3),
                                               (40, 1024, 16, 0, 3, 4)])
 def test_permute_rows_and_fp8(oracle, dev, T, H, E, k, pad, seed):
