@@ -358,50 +358,6 @@ def main():
         }
         del xe, pe
 
-    if want("permute"):
-        # TE's moe_permute on an MXFP4 tensor at one rank's share: 4096 tokens routed top-8 of 64
-        # experts (seeded), H = 7168, 32768 expert-major output rows. The row map is built once
-        # (make_row_id_map synchronizes with the host); timed are the gather, the gather fused
-        # into the FP8 requant, and the gather followed by the requant (eager launches).
-        import omo
-        from omo_python_api import permutation as pm
-        from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
-        from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToFp8_wrapper
-        Tq, Hq, Eq, topk = 4096, K, 64, 8
-        gq = torch.Generator(device="cpu").manual_seed(81)
-        rmap = torch.zeros((Tq, Eq), dtype=torch.bool)
-        rmap.scatter_(1, torch.rand((Tq, Eq), generator=gq).topk(topk, dim=1).indices, True)
-        cq, csq = omo_per_token_group_quant_mxfp4(wl.normal_bf16((Tq, Hq), seed=82, device=dev))
-        src, _, _ = pm.make_row_id_map(rmap.to(dev))
-        Np = src.numel()
-        gq_out = (torch.empty((Np, Hq // 2), dtype=torch.uint8, device=dev),
-                  torch.empty((Np, Hq // 32), dtype=torch.uint8, device=dev))
-        fq_out = (torch.empty((Np, Hq), dtype=torch.float8_e4m3fn, device=dev),
-                  torch.empty((Hq // 128, Np), dtype=torch.float32, device=dev))
-
-        def unfused(_i):
-            omo.omo_mxfp4_permute_rows(cq, csq, src, *gq_out)
-            return omo_per_token_mxfp4ToFp8_wrapper(*gq_out, [Np])
-
-        row_b, fp8_b = Hq // 2 + Hq // 32, Hq + Hq // 128 * 4
-        steps = max(100, args.steps // 4)
-        res = {}
-        for name, fn in [("gather", lambda i: omo.omo_mxfp4_permute_rows(cq, csq, src, *gq_out)),
-                         ("gather_to_fp8_fused", lambda i: omo.omo_permute_Mxfp4ToFp8(cq, csq, src, *fq_out)),
-                         ("gather_then_fp8", unfused)]:
-            t, _ = time_launches(torch, fn, 1, steps, 10, graph=False)
-            res[name] = round(t / steps * 1e3, 2)
-        out["permute"] = {
-            "workload": f"MXFP4 moe_permute, {Tq} tokens top-{topk} of {Eq} experts -> {Np} rows, H={Hq} "
-                        "(eager launches, us per call)",
-            "us": res,
-            "fused_speedup": round(res["gather_then_fp8"] / res["gather_to_fp8_fused"], 3),
-            "gather_GB/s": round(2 * Np * row_b / (res["gather"] * 1e-6) / 1e9, 1),
-            "gather_to_fp8_fused_GB/s": round(Np * (row_b + fp8_b) / (res["gather_to_fp8_fused"] * 1e-6) / 1e9, 1),
-            "bytes": "rows moved: gather 2 x rows x (H/2 + H/32); fused rows x (H/2 + H/32 + H + 4H/128)",
-        }
-        del cq, csq, gq_out, fq_out
-
     if want("moe"):
         # cfg5: one MoE layer's MXFP4 codec work on the GPU that owns experts 0-7 of 64
         # (16384 tokens, top-8 of 64, seeded): per-expert rows m_e (ragged, ~2048 each),
@@ -502,6 +458,50 @@ def main():
         out["row_to_col_fp8"] = {"workload": "MXFP4 rowwise -> FP8 columnwise 4096x7168",
                                  "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
                                  "us_per_launch": round(t / steps * 1e3, 2)}
+
+    if want("permute"):
+        # TE's moe_permute on an MXFP4 tensor at one rank's share: 4096 tokens routed top-8 of 64
+        # experts (seeded), H = 7168, 32768 expert-major output rows. The row map is built once
+        # (make_row_id_map synchronizes with the host); timed are the gather, the gather fused
+        # into the FP8 requant, and the gather followed by the requant (eager launches).
+        import omo
+        from omo_python_api import permutation as pm
+        from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
+        from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToFp8_wrapper
+        Tq, Hq, Eq, topk = 4096, K, 64, 8
+        gq = torch.Generator(device="cpu").manual_seed(81)
+        rmap = torch.zeros((Tq, Eq), dtype=torch.bool)
+        rmap.scatter_(1, torch.rand((Tq, Eq), generator=gq).topk(topk, dim=1).indices, True)
+        cq, csq = omo_per_token_group_quant_mxfp4(wl.normal_bf16((Tq, Hq), seed=82, device=dev))
+        src, _, _ = pm.make_row_id_map(rmap.to(dev))
+        Np = src.numel()
+        gq_out = (torch.empty((Np, Hq // 2), dtype=torch.uint8, device=dev),
+                  torch.empty((Np, Hq // 32), dtype=torch.uint8, device=dev))
+        fq_out = (torch.empty((Np, Hq), dtype=torch.float8_e4m3fn, device=dev),
+                  torch.empty((Hq // 128, Np), dtype=torch.float32, device=dev))
+
+        def unfused(_i):
+            omo.omo_mxfp4_permute_rows(cq, csq, src, *gq_out)
+            return omo_per_token_mxfp4ToFp8_wrapper(*gq_out, [Np])
+
+        row_b, fp8_b = Hq // 2 + Hq // 32, Hq + Hq // 128 * 4
+        steps = max(100, args.steps // 4)
+        res = {}
+        for name, fn in [("gather", lambda i: omo.omo_mxfp4_permute_rows(cq, csq, src, *gq_out)),
+                         ("gather_to_fp8_fused", lambda i: omo.omo_permute_Mxfp4ToFp8(cq, csq, src, *fq_out)),
+                         ("gather_then_fp8", unfused)]:
+            t, _ = time_launches(torch, fn, 1, steps, 10, graph=False)
+            res[name] = round(t / steps * 1e3, 2)
+        out["permute"] = {
+            "workload": f"MXFP4 moe_permute, {Tq} tokens top-{topk} of {Eq} experts -> {Np} rows, H={Hq} "
+                        "(eager launches, us per call)",
+            "us": res,
+            "fused_speedup": round(res["gather_then_fp8"] / res["gather_to_fp8_fused"], 3),
+            "gather_GB/s": round(2 * Np * row_b / (res["gather"] * 1e-6) / 1e9, 1),
+            "gather_to_fp8_fused_GB/s": round(Np * (row_b + fp8_b) / (res["gather_to_fp8_fused"] * 1e-6) / 1e9, 1),
+            "bytes": "rows moved: gather 2 x rows x (H/2 + H/32); fused rows x (H/2 + H/32 + H + 4H/128)",
+        }
+        del cq, csq, gq_out, fq_out
 
     if want("ceiling"):
         try:
