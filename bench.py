@@ -9,7 +9,7 @@ resident in HBM before the timed region. Four input/output buffer sets
 set. The script prints one JSON line.
 
 Also measured (extra keys): MXFP4 -> BF16 dequant of the same shape, the
-MoE-payload requant/dequant (4096 x 7168, both FP8 layouts), the fused
+cfg1 quantize + dequantize round trip (4096 x 4096), the MoE-payload requant/dequant (4096 x 7168, both FP8 layouts), the fused
 expert-parallel payload rows against Megatron's cat/split composition, the
 MXFP4 moe_permute gather (alone and fused into the FP8 requant), the
 cfg5 MoE layer composite (all codec launches of one layer on 8 local experts),
@@ -18,8 +18,13 @@ each as GB/s of algorithmic bytes or microseconds per call, and memory-only
 kernels over the headline buffers (the quantize's loads and stores without
 its arithmetic; streaming reads; streaming writes) as the practical bound.
 
+The CPU baseline runs the oracle (a multithreaded C restatement of the
+reference kernels) on the host's cores for the headline quantize and, in the
+legs that have one, for cfg1's round trip, the cfg2 dequant and cfg4's FP8
+requant and dequant; each of those also checks the GPU outputs against it.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-       [--only quant|dequant|...] [--copy-calibration]
+       [--only headline|dequant,cfg1,...] [--copy-calibration]
 """
 import argparse
 import json
@@ -43,7 +48,8 @@ def parse():
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (>= 3 to exceed the 256 MB cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="comma list of legs: quant,dequant,payload,ep_payload,permute,moe,dual,rowcol,ceiling")
+                    help="comma list of extra legs: dequant,cfg1,payload,ep_payload,permute,moe,dual,rowcol,"
+                         "ceiling; 'headline' runs the headline quantize alone")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (known traffic) for counter calibration")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -86,6 +92,50 @@ def cpu_model():
     except OSError:
         pass
     return None
+
+
+def cpu_threads():
+    """Threads for the CPU baseline and what bounds them. The oracle runs on
+    every CPU this process may use (its affinity mask), capped by the cgroup
+    CPU quota and by OMP_NUM_THREADS where the host sets them: on a shared GPU
+    host those state this GPU's share of the cores. Returns (threads, info)."""
+    info = {"host_logical_cpus": os.cpu_count()}
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count() or 1
+    info["affinity_cpus"] = aff
+    n = aff
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, int(q) // int(period))
+    except (OSError, ValueError):
+        pass
+    info["cgroup_cpu_quota"] = quota
+    if quota:
+        n = min(n, quota)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    info["omp_num_threads"] = int(omp) if omp.isdigit() and int(omp) > 0 else None
+    if info["omp_num_threads"]:
+        n = min(n, info["omp_num_threads"])
+    info["threads_used"] = n
+    return n, info
+
+
+def cpu_time(fn, seconds, min_reps=3, max_reps=2000):
+    """Runs fn repeatedly for about `seconds` (at least min_reps times);
+    returns (last result, median seconds per call, reps, total seconds)."""
+    times = []
+    res = None
+    t_end = time.time() + seconds
+    while len(times) < min_reps or (time.time() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        res = fn()
+        times.append(time.perf_counter() - t0)
+    return res, statistics.median(times), len(times), sum(times)
 
 
 def sets_for(bytes_per_set, minimum):
@@ -226,31 +276,41 @@ def main():
 
     # parity of the timed outputs (set 0) against the CPU oracle, and the CPU baseline
     cpu = None
-    parity = None
+    parity = {}
+    oracle = np = None
+    nthreads, thread_info = cpu_threads()
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import numpy as np
         import oracle
         xb = xs[0].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1)
-        nthreads = min(16, os.cpu_count() or 1)
-        times = []
-        t_end = time.time() + args.cpu_seconds
-        while len(times) < 3 or (time.time() < t_end and len(times) < 2000):
-            t0 = time.perf_counter()
-            eq, es = oracle.quant_mxfp4(xb, nthreads=nthreads)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        parity = bool(np.array_equal(qs[0].cpu().numpy().reshape(-1), eq) and
-                      np.array_equal(ss[0].cpu().numpy().reshape(-1), es))
+        (eq, es), med, reps, spent = cpu_time(lambda: oracle.quant_mxfp4(xb, nthreads=nthreads), args.cpu_seconds)
+        parity["quant_cfg2"] = bool(np.array_equal(qs[0].cpu().numpy().reshape(-1), eq) and
+                                    np.array_equal(ss[0].cpu().numpy().reshape(-1), es))
         cpu = {"value": round(qbytes / med / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-               "sample": f"oracle quantize of the full 8192x7168 cfg2 tensor, {len(times)} reps, median "
-                         f"{med * 1e3:.1f} ms ({sum(times):.1f} s of CPU work)", "cpu_model": cpu_model()}
+               "sample": f"oracle quantize of the full 8192x7168 cfg2 tensor on {nthreads} threads, {reps} reps, "
+                         f"median {med * 1e3:.1f} ms ({spent:.1f} s of CPU work)",
+               "cpu_model": cpu_model(), **thread_info, "per_config": {}}
 
-    traffic = None
+    def cpu_leg(name, fn, nbytes, check=None, seconds=None):
+        """Times the oracle on one more configuration (bounded CPU time) and
+        checks the GPU outputs against its result."""
+        if cpu is None:
+            return
+        res, med, reps, spent = cpu_time(fn, seconds or max(1.0, args.cpu_seconds / 4))
+        cpu["per_config"][name] = {"GB/s": round(nbytes / med / 1e9, 3), "median_ms": round(med * 1e3, 2),
+                                   "reps": reps, "cpu_s": round(spent, 1)}
+        if check is not None:
+            parity[name] = bool(check(res))
+
+    traffic, traffic_source = None, None
     tpath = os.path.join(ROOT, "profiles", "traffic_quant_phased_cfg2.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            tj = json.load(f)
+        traffic = tj.get("hbm_bytes_per_launch")
+        traffic_source = {"file": "profiles/traffic_quant_phased_cfg2.json",
+                          **{k: tj.get(k) for k in ("measured_at_commit", "library_sha256_16", "command")}}
 
     # ---- extra legs -------------------------------------------------------
     if want("dequant"):
@@ -268,7 +328,48 @@ def main():
         out["dequant"] = {"workload": "MXFP4->BF16 8192x7168", "GB/s": round(dq / (t / steps * 1e-3) / 1e9, 1),
                           "us_per_launch": round(t / steps * 1e3, 2),
                           "frac_of_peak": round(dq / (t / steps * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if cpu is not None:
+            y0 = ys[0].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+            cpu_leg("dequant_cfg2", lambda: oracle.dequant_bf16(eq, es, nthreads=nthreads), dq,
+                    check=lambda r: np.array_equal(r, y0))
         del ys
+
+    if want("cfg1"):
+        # cfg1: quantize + dequantize round trip of the seeded 4096 x 4096 N(0,1) tensor
+        M1, K1 = wl.CFG1_SHAPE
+        n1 = M1 * K1
+        b1 = wl.quant_bytes(n1) + wl.dequant_bytes(n1)
+        c1s = sets_for(b1, args.sets)
+        x1 = [wl.cfg1_input(device=dev)] + [wl.normal_bf16((M1, K1), seed=wl.CFG1_SEED + i, device=dev)
+                                             for i in range(1, c1s)]
+        q1 = [torch.empty((M1, K1 // 2), dtype=torch.uint8, device=dev) for _ in range(c1s)]
+        s1 = [torch.empty((M1, K1 // 32), dtype=torch.uint8, device=dev) for _ in range(c1s)]
+        y1 = [torch.empty((M1, K1), dtype=torch.bfloat16, device=dev) for _ in range(c1s)]
+
+        def round_trip(i):
+            _abi.check(lib.omo_hip_per_token_group_quant_fp4(x1[i].data_ptr(), n1, q1[i].data_ptr(), n1 // 2,
+                                                             s1[i].data_ptr(), n1 // 32, 32, 1e-10, -6.0, 6.0, 0,
+                                                             cur()))
+            _abi.check(lib.omo_hip_per_token_Mxfp4ToBf16_dequant(q1[i].data_ptr(), n1 // 2, s1[i].data_ptr(),
+                                                                 n1 // 32, y1[i].data_ptr(), n1, None, 0, 32, 1e-10,
+                                                                 -6.0, 6.0, 0, cur()))
+        steps = max(100, args.steps // 4)
+        t, _ = time_launches(torch, round_trip, c1s, steps, 20)
+        out["cfg1_round_trip"] = {"workload": "cfg1 quantize + dequantize round trip, 4096x4096 N(0,1) bf16",
+                                  "GB/s": round(b1 / (t / steps * 1e-3) / 1e9, 1),
+                                  "us_per_round_trip": round(t / steps * 1e3, 2),
+                                  "algorithmic_bytes": b1}
+        if cpu is not None:
+            xb1 = x1[0].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+            got = (q1[0].cpu().numpy().reshape(-1), s1[0].cpu().numpy().reshape(-1),
+                   y1[0].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1))
+
+            def cpu_round_trip():
+                cq_, cs_ = oracle.quant_mxfp4(xb1, nthreads=nthreads)
+                return cq_, cs_, oracle.dequant_bf16(cq_, cs_, nthreads=nthreads)
+            cpu_leg("cfg1_round_trip", cpu_round_trip, b1,
+                    check=lambda r: all(np.array_equal(a, b) for a, b in zip(r, got)))
+        del x1, q1, s1, y1
 
     if want("payload"):
         # cfg4: one GPU's share of the MoE dispatch payload, requant to FP8 and dequant to bf16
@@ -308,6 +409,15 @@ def main():
         out["payload_dequant_bf16"] = {"workload": "MXFP4->BF16 4096x7168",
                                        "kernel_GB/s": round(db / (t / steps * 1e-3) / 1e9, 1),
                                        "us_per_launch": round(t / steps * 1e3, 2)}
+        if cpu is not None:
+            qn, sn = q4[0].cpu().numpy(), s4[0].cpu().numpy()
+            f8g = (f8[0].cpu().view(torch.uint8).numpy(), f8s[0].cpu().numpy())
+            y4g = y4[0].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+            cpu_leg("cfg4_requant_fp8", lambda: oracle.mxfp4_to_fp8(qn, sn, nthreads=nthreads), rb,
+                    check=lambda r: np.array_equal(r[0], f8g[0]) and np.array_equal(r[1].view(np.uint32),
+                                                                                     f8g[1].view(np.uint32)))
+            cpu_leg("cfg4_dequant_bf16", lambda: oracle.dequant_bf16(qn, sn, nthreads=nthreads), db,
+                    check=lambda r: np.array_equal(r, y4g))
         # transposed FP8 requant (fp8 [2W, M] + fp32 [M/128, 2W]) of the same payload
         fc = [torch.empty((K, Mp), dtype=torch.float8_e4m3fn, device=dev) for _ in range(ps)]
         fcs = [torch.empty((Mp // 128, K), dtype=torch.float32, device=dev) for _ in range(ps)]
@@ -340,9 +450,9 @@ def main():
         res = {}
         for name, fn in [
             ("send_fused", lambda i: ep.fp4_quantize_packed(xe[i])),
-            ("send_unfused", lambda i: ep.pack_rowwise_components(*omo_per_token_group_quant_mxfp4(xe[i]))),
+            ("send_unfused", lambda i: ep.join_payload(*omo_per_token_group_quant_mxfp4(xe[i]))),
             ("recv_fp8_fused", lambda i: ep.packed_mxfp4ToFp8(pe[i])),
-            ("recv_fp8_unfused", lambda i: omo_per_token_mxfp4ToFp8_wrapper(*ep.unpack_rowwise_components(pe[i]),
+            ("recv_fp8_unfused", lambda i: omo_per_token_mxfp4ToFp8_wrapper(*ep.split_payload(pe[i]),
                                                                              [Tp])),
             ("recv_bf16_fused", lambda i: ep.packed_mxfp4ToBf16(pe[i])),
         ]:
@@ -528,9 +638,11 @@ def main():
                    "input_sha256": input_sha256},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_source,
                      "kernel": "quant_phased_kernel", "avg_launch_us": round(avg_launch_ms * 1e3, 3)},
         "cpu_baseline": cpu,
-        "parity_vs_oracle": parity,
+        "parity_vs_oracle": all(parity.values()) if parity else None,
+        "parity_detail": parity or None,
         "timing": "eager launches" if args.eager else "one HIP-graph replay of the timed launches",
     }
     line.update(out)

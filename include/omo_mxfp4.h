@@ -115,8 +115,13 @@ OMO_API int omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(const void* input, int64_t 
 /* Grouped (per-expert) variant with power-of-two scales. m_splits,
  * split_offsets and scale_offsets are int32 device arrays of num_splits
  * entries; split i's output is a contiguous [N, m_splits[i]] block at
- * split_offsets[i]*N. Tiles whose metadata points outside the buffers are
- * skipped on the device.
+ * split_offsets[i]*N. The metadata stays on the device, so the host cannot
+ * check it: tiles whose metadata points outside the buffers (split_offsets[i]
+ * + m_splits[i] > rows, or scale_offsets[i] + ceil(m_splits[i]/128) >
+ * output_s rows) are skipped on the device, that split's output is then left
+ * partly or wholly unwritten, and the call still returns OMO_OK. Callers
+ * building the arrays on the host check those two bounds first (the Python
+ * wrapper derives them from m_splits, where they hold by construction).
  * Replaces omo::omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit
  * (code/kernel/per_token_Mxfp4RowToBf16ToFp8Col_msplit.cu:232-283; binding code/kernel/ops.cu:38-39). */
 OMO_API int omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(const void* input, int64_t rows, int64_t row_bytes,

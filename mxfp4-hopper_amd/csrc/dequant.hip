@@ -114,10 +114,9 @@ hipError_t launch_dequant_rows(const void* q, int64_t q_stride, const void* s, i
   if (rows == 0 || K == 0) return hipSuccess;
   constexpr int U = 4;
   const int bpr = (int)((K / 8 + 256 * U - 1) / (256 * U));
-  hipLaunchKernelGGL((dequant_rows_kernel<U>), dim3((unsigned)(rows * bpr)), dim3(256), 0, stream,
+  return launch((dequant_rows_kernel<U>), dim3((unsigned)(rows * bpr)), dim3(256), 0, stream,
                      static_cast<const uint8_t*>(q), q_stride, static_cast<const uint8_t*>(s), s_stride,
                      static_cast<u32x4*>(out), K, bpr);
-  return hipGetLastError();
 }
 
 hipError_t launch_dequant_bf16(const void* q, const void* s, void* out, int64_t nbytes, hipStream_t stream) {
@@ -125,9 +124,8 @@ hipError_t launch_dequant_bf16(const void* q, const void* s, void* out, int64_t 
   if (ndw == 0) return hipSuccess;
   constexpr int U = 4;
   const int64_t blocks = (ndw + 256 * U - 1) / (256 * U);
-  hipLaunchKernelGGL((dequant_bf16_kernel<U>), dim3((unsigned)blocks), dim3(256), 0, stream,
+  return launch((dequant_bf16_kernel<U>), dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<u32x4*>(out), ndw);
-  return hipGetLastError();
 }
 
 }  // namespace omo_hip

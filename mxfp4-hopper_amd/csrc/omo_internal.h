@@ -5,8 +5,27 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <cstring>
+#include <tuple>
+#include <type_traits>
+#include <utility>
 
 namespace omo_hip {
+
+// Enqueues `kernel` with its arguments converted to the kernel's parameter
+// types and returns the status of this launch alone (hipLaunchKernel's return
+// value), so an error left earlier on the calling thread by other code is
+// neither reported as this launch's failure nor cleared.
+template <typename... P, typename... A>
+hipError_t launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t stream, A&&... args) {
+  static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+  std::tuple<std::decay_t<P>...> vals(static_cast<std::decay_t<P>>(std::forward<A>(args))...);
+  return std::apply(
+      [&](auto&... v) {
+        void* ptrs[] = {static_cast<void*>(&v)...};
+        return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, lds, stream);
+      },
+      vals);
+}
 
 hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, float eps, float fp4_min,
                                 float fp4_max, hipStream_t stream);

@@ -276,13 +276,11 @@ hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, 
       p.fp4_min = -6.0f;
       p.fp4_max = 6.0f;
       p.c_eps = a.c_eps;
-      hipLaunchKernelGGL(quant_phased_rows_kernel, dim3((unsigned)grid), dim3(kPhThreads), (size_t)lds, stream, p,
+      return launch(quant_phased_rows_kernel, dim3((unsigned)grid), dim3(kPhThreads), (size_t)lds, stream, p,
                          a.q, rows, (int)rpw, (int)cpr);
-      return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((quant_rows_kernel<U>), dim3((unsigned)(rows * a.bpr)), dim3(256), 0, stream, a);
-  return hipGetLastError();
+  return launch((quant_rows_kernel<U>), dim3((unsigned)(rows * a.bpr)), dim3(256), 0, stream, a);
 }
 
 hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, float eps, float fp4_min,
@@ -316,16 +314,11 @@ hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, 
   const double fill = (double)a.nchunks / ((double)dc.cus * kPhThreads * kPhUnroll * (double)steps);
   if (standard && aligned16 && share >= 4096 && share <= cap && fill >= 0.95) {
     const int round = (int)share;
-    hipLaunchKernelGGL(quant_phased_kernel, dim3((unsigned)dc.cus), dim3(kPhThreads), (size_t)round * 4 + round / 4,
+    return launch(quant_phased_kernel, dim3((unsigned)dc.cus), dim3(kPhThreads), (size_t)round * 4 + round / 4,
                        stream, a, share, round);
-    return hipGetLastError();
   }
-  if (standard) {
-    hipLaunchKernelGGL((quant_rowwise_kernel<U, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((quant_rowwise_kernel<U, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  }
-  return hipGetLastError();
+  auto kernel = standard ? quant_rowwise_kernel<U, true> : quant_rowwise_kernel<U, false>;
+  return launch(kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 
 }  // namespace omo_hip

@@ -415,18 +415,16 @@ hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_
   const int64_t tiles = tiles_m * tiles_k;
   if (dual_super_ok(x, row_q, col_q, M, K)) {
     const int64_t sm = (M + kSuperRows - 1) / kSuperRows, st = sm * tiles_k, spx = (st + kXcds - 1) / kXcds;
-    hipLaunchKernelGGL(quant_dual_super_kernel, dim3((unsigned)(spx * kXcds)), dim3(kDualThreads), 0, stream,
+    return launch(quant_dual_super_kernel, dim3((unsigned)(spx * kXcds)), dim3(kDualThreads), 0, stream,
                        static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
                        static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, (int)sm, (int)st, (int)spx,
                        eps, host_c_eps(eps, 6.0f));
-    return hipGetLastError();
   }
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
-  hipLaunchKernelGGL(quant_dual_kernel, dim3((unsigned)(per_xcd * kXcds)), dim3(kDualThreads), 0, stream,
+  return launch(quant_dual_kernel, dim3((unsigned)(per_xcd * kXcds)), dim3(kDualThreads), 0, stream,
                      static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
                      static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, (int)tiles_m, (int)tiles,
                      (int)per_xcd, eps, host_c_eps(eps, 6.0f));
-  return hipGetLastError();
 }
 
 hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps, hipStream_t stream) {
@@ -460,14 +458,8 @@ hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps
     g.per_xcd = (tiles + kXcds - 1) / kXcds;
     g.eps = eps;
     g.c_eps = host_c_eps(eps, 6.0f);
-    if (super) {
-      hipLaunchKernelGGL(quant_dual_grouped_super_kernel, dim3((unsigned)(g.per_xcd * kXcds)), dim3(kDualThreads), 0,
-                         stream, g);
-    } else {
-      hipLaunchKernelGGL(quant_dual_grouped_kernel, dim3((unsigned)(g.per_xcd * kXcds)), dim3(kDualThreads), 0, stream,
-                         g);
-    }
-    const hipError_t e = hipGetLastError();
+    auto kernel = super ? quant_dual_grouped_super_kernel : quant_dual_grouped_kernel;
+    const hipError_t e = launch(kernel, dim3((unsigned)(g.per_xcd * kXcds)), dim3(kDualThreads), 0, stream, g);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -168,10 +168,9 @@ hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void*
   const int64_t gx = (gpr + kRqGroups - 1) / kRqGroups, gy = (M + kRqRows - 1) / kRqRows;
   const bool a8 = (q_stride % 8 == 0) && ((reinterpret_cast<uintptr_t>(q) & 7) == 0);
   auto kernel = a8 ? mxfp4_to_fp8_kernel<U, true> : mxfp4_to_fp8_kernel<U, false>;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q), q_stride,
+  return launch(kernel, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q), q_stride,
                      static_cast<const uint8_t*>(s), s_stride, src, n_src, static_cast<u32x4*>(out), out_s,
                      (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
-  return hipGetLastError();
 }
 
 hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,
@@ -315,9 +314,8 @@ hipError_t launch_mxfp4_to_fp8_col(const void* q, const void* s, void* out, floa
   if (eps > 0.0f) eps8 = eps >= 255.0f ? 255u : (uint32_t)eps;  // (uint8_t)eps, truncating
   // 1-D grid, tile index bx fastest, renumbered per XCD in the kernel
   const dim3 grid((unsigned)((Kb / kColTile) * (M / kColTile)));
-  hipLaunchKernelGGL(mxfp4_to_fp8_col_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
+  return launch(mxfp4_to_fp8_col_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, M, Kb, eps8);
-  return hipGetLastError();
 }
 
 }  // namespace omo_hip

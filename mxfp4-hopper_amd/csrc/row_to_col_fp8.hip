@@ -730,9 +730,8 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
   if (vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
     const dim3 grid((unsigned)(((M + kTile - 1) / kTile) * (N / kWideCols)));
     auto kernel = full ? row_to_fp8_col_wide_kernel<false> : row_to_fp8_col_wide_kernel<true>;
-    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s),
+    return launch(kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s),
                        static_cast<uint8_t*>(out), out_s, M, N, eps);
-    return hipGetLastError();
   }
   const int64_t tiles_m = (M + kTile - 1) / kTile, tiles = tiles_m * ((N + kTile - 1) / kTile);
   // one wave of resident blocks: two 512-thread blocks per CU at this
@@ -740,10 +739,9 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
   const int64_t grid_cap = 2 * (int64_t)current_device_caps().cus;
   const int64_t grid = tiles < grid_cap ? tiles : grid_cap;
   auto kernel = full ? row_to_fp8_col_kernel<true> : row_to_fp8_col_kernel<false>;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
+  return launch(kernel, dim3((unsigned)grid), dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, M, N, (int)tiles_m, (int)tiles,
                      eps, vin, vs);
-  return hipGetLastError();
 }
 
 hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out, float* out_s, int64_t total_rows,
@@ -762,16 +760,14 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
     // 62.8 right after a 512 MB fill (dirty caches, as in a layer step).
     const int per_wg = current_device_caps().lds_per_workgroup / 4 - 2560;
     const size_t reserve = per_wg > (int)sizeof(WideSmem) ? (size_t)(per_wg - (int)sizeof(WideSmem)) : 0;
-    hipLaunchKernelGGL(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
+    return launch(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
                        static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs,
                        total_rows, N, out_s_rows, eps, (reinterpret_cast<uintptr_t>(out) & 127) == 0);
-    return hipGetLastError();
   }
   dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)((N + kTile - 1) / kTile));
-  hipLaunchKernelGGL(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
+  return launch(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
                      out_s_rows, eps, vin, vs);
-  return hipGetLastError();
 }
 
 }  // namespace omo_hip

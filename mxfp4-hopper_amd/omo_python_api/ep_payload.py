@@ -1,16 +1,17 @@
 """Expert-parallel MXFP4 payload rows: [codes (H/2 bytes) | E8M0 scales (H/32 bytes)].
 
-Megatron's FP4 path (code/megatron-0.15.0rc7.diff:32-63, 163-170) quantizes the
-tokens it sends through DeepEP, concatenates codes and scales along the last
-dimension (``torch.cat``), and on the receiving side splits the payload again
-with two ``.contiguous()`` copies before requantizing or dequantizing it.
+Megatron's FP4 dispatch (code/megatron-0.15.0rc7.diff:32-63, 91-124) sends each
+token as one row of H/2 code bytes followed by its H/32 scale bytes, 17H/32
+bytes in all. Its send side builds those rows by concatenating the quantize
+outputs; its receive side cuts them apart again into two contiguous tensors
+before the requant or dequant.
 
-``pack_rowwise_components`` / ``unpack_rowwise_components`` keep that
-behaviour (same checks and errors) for callers that hold the pieces. The
-``*_packed`` functions are the fused path: the quantize kernel writes payload
-rows directly and the dequant / FP8 requant kernels read them in place, so the
-concatenation and both split copies disappear. Their outputs are byte-identical
-to the unfused composition.
+``join_payload`` / ``split_payload`` are that unfused composition, kept as the
+comparison for the fused path and for callers that hold separate code and
+scale tensors. The ``*_packed`` functions are the fused path: the quantize
+kernel writes payload rows directly and the dequant / FP8 requant kernels read
+them in place, so neither the concatenation nor the two split copies happen.
+Their outputs are byte-identical to the unfused composition.
 """
 from typing import List, Optional, Tuple
 
@@ -18,53 +19,46 @@ import torch
 
 from omo import omo_packed_Mxfp4ToBf16_dequant, omo_packed_Mxfp4ToFp8, omo_quant_mxfp4_packed
 
-FP4_VALUES_PER_SCALE = 16  # code bytes per scale byte (megatron-0.15.0rc7.diff:17)
-
-
-def pack_rowwise_components(rowwise_data: torch.Tensor, rowwise_scale: torch.Tensor) -> torch.Tensor:
-    """_pack_rowwise_components (megatron-0.15.0rc7.diff:93-99)."""
-    if rowwise_data.shape[:-1] != rowwise_scale.shape[:-1]:
-        raise ValueError("rowwise_data and rowwise_scale_inv must match on all dims except the last.")
-    return torch.cat((rowwise_data, rowwise_scale), dim=-1)
-
-
-def unpack_rowwise_components(packed_tensor: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """_unpack_rowwise_components (megatron-0.15.0rc7.diff:101-122): the code
-    width is last_dim * 16 / 17; both parts are returned as contiguous copies."""
-    if packed_tensor.dim() < 1:
-        raise ValueError("Packed FP4 tensor must have at least one dimension.")
-    last_dim = packed_tensor.size(-1)
-    numerator = last_dim * FP4_VALUES_PER_SCALE
-    divisor = FP4_VALUES_PER_SCALE + 1
-    if numerator % divisor != 0:
-        raise ValueError(
-            f"Cannot infer FP4 rowwise/scale split for last_dim={last_dim}. "
-            "Dimension must be divisible by the 17/16 packing ratio.")
-    rowwise_width = numerator // divisor
-    scale_width = last_dim - rowwise_width
-    if scale_width <= 0:
-        raise ValueError("Packed FP4 tensor does not contain scale elements.")
-    rowwise_data = packed_tensor.narrow(-1, 0, rowwise_width).contiguous()
-    rowwise_scale = packed_tensor.narrow(-1, rowwise_width, scale_width).contiguous()
-    return rowwise_data, rowwise_scale
-
 
 def payload_width(hidden: int) -> int:
     """Bytes per payload row for hidden size H: H/2 + H/32 = 17H/32."""
     return hidden // 2 + hidden // 32
 
 
-def _hidden_of(packed: torch.Tensor) -> int:
-    width = packed.size(-1)
-    if width % 17 != 0:
+def hidden_of(packed: torch.Tensor) -> int:
+    """Hidden size H of payload rows [T, 17H/32] (H a multiple of 32)."""
+    if packed.dim() != 2:
+        raise ValueError(f"payload must be 2-D [tokens, 17H/32], got {packed.dim()} dims")
+    width = packed.size(1)
+    if width == 0 or width % 17 != 0:
         raise ValueError(f"payload width {width} is not 17/32 of a hidden size")
     return width // 17 * 32
+
+
+def join_payload(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """Payload rows from separate rowwise codes [T, H/2] and scale bytes
+    [T, H/32]: one concatenation along the row (the unfused send side)."""
+    if codes.dim() != 2 or scales.dim() != 2:
+        raise ValueError("codes and scales must both be 2-D [tokens, bytes]")
+    if codes.size(0) != scales.size(0):
+        raise ValueError(f"codes hold {codes.size(0)} tokens but scales hold {scales.size(0)}")
+    if codes.size(1) != 16 * scales.size(1):
+        raise ValueError(f"{codes.size(1)} code bytes per token need {codes.size(1) // 16} scale bytes, "
+                         f"got {scales.size(1)}")
+    return torch.cat((codes, scales), dim=1)
+
+
+def split_payload(packed: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Contiguous codes [T, H/2] and scale bytes [T, H/32] cut out of payload
+    rows (the unfused receive side: two copies)."""
+    half = hidden_of(packed) // 2
+    return packed[:, :half].contiguous(), packed[:, half:].contiguous()
 
 
 def fp4_quantize_packed(x: torch.Tensor, eps: float = 1e-10) -> torch.Tensor:
     """Fused ``fp4_quantize`` (megatron-0.15.0rc7.diff:163-170): bf16 [T, H]
     (H % 128 == 0) -> payload [T, 17H/32] uint8, equal to
-    pack_rowwise_components(*omo_per_token_group_quant_mxfp4(x))."""
+    join_payload(*omo_per_token_group_quant_mxfp4(x))."""
     assert x.dim() == 2, "`x` must be 2-D [tokens, hidden]"
     assert x.is_contiguous(), "`x` is not contiguous"
     T, H = x.shape
@@ -76,10 +70,9 @@ def fp4_quantize_packed(x: torch.Tensor, eps: float = 1e-10) -> torch.Tensor:
 
 def packed_mxfp4ToBf16(packed: torch.Tensor, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """Payload [T, 17H/32] -> [T, H] in ``dtype``, equal to
-    omo_per_token_mxfp4ToBf16_dequant_wrapper(*unpack_rowwise_components(packed), dtype)."""
-    assert packed.dim() == 2, "payload must be 2-D [tokens, 17H/32]"
+    omo_per_token_mxfp4ToBf16_dequant_wrapper(*split_payload(packed), dtype)."""
     assert packed.is_contiguous(), "payload is not contiguous"
-    T, H = packed.size(0), _hidden_of(packed)
+    T, H = packed.size(0), hidden_of(packed)
     out = torch.empty((T, H), device=packed.device, dtype=torch.bfloat16)
     if T > 0:
         omo_packed_Mxfp4ToBf16_dequant(packed, out)
@@ -91,9 +84,8 @@ def packed_mxfp4ToFp8(packed: torch.Tensor, m_splits: Optional[List[int]] = None
     by ``m_splits`` along tokens as omo_per_token_mxfp4ToFp8_wrapper does
     (code/kernel/api/mxfp4_dequant.py:172-181); without m_splits the whole
     tensors are returned."""
-    assert packed.dim() == 2, "payload must be 2-D [tokens, 17H/32]"
     assert packed.is_contiguous(), "payload is not contiguous"
-    T, H = packed.size(0), _hidden_of(packed)
+    T, H = packed.size(0), hidden_of(packed)
     x_q = torch.empty((T, H), device=packed.device, dtype=torch.float8_e4m3fn)
     x_s = torch.empty((H // 128, T), device=packed.device, dtype=torch.float32)
     if T > 0:

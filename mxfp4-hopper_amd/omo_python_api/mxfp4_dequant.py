@@ -147,6 +147,8 @@ def split_metadata(m_splits: List[int], device) -> tuple:
     longest split, as the msplit kernel expects them
     (code/kernel/per_token_Mxfp4RowToBf16ToFp8Col_msplit.cu:74-80, 256)."""
     lens = [int(m) for m in m_splits]
+    if any(m < 0 for m in lens):
+        raise ValueError(f"m_splits must be non-negative, got {lens}")
     offs, soffs, o, so = [], [], 0, 0
     for m in lens:
         offs.append(o)

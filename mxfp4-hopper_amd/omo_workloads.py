@@ -12,8 +12,6 @@ distributions are those of the benchmark configurations:
 """
 from __future__ import annotations
 
-import math
-
 import torch
 
 
@@ -29,6 +27,16 @@ def normal_bf16(shape, seed: int, device="cpu", std: float = 1.0) -> torch.Tenso
     if std != 1.0:
         x.mul_(std)
     return x.to(torch.bfloat16)
+
+
+CFG1_SHAPE = (4096, 4096)
+CFG1_SEED = 4096
+
+
+def cfg1_input(device="cpu") -> torch.Tensor:
+    """cfg1: the seeded 4096 x 4096 N(0,1) bf16 tensor of the quantize +
+    dequantize round trip."""
+    return normal_bf16(CFG1_SHAPE, seed=CFG1_SEED, device=device)
 
 
 def activations_with_outliers(M: int, K: int, seed: int, device="cpu", frac: float = 0.001,
@@ -103,4 +111,3 @@ def row_to_col_fp8_bytes(M: int, N: int) -> int:
 
 
 __all__ = [name for name in dir() if not name.startswith("_") and name != "annotations"]
-_ = math

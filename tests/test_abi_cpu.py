@@ -7,6 +7,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -152,23 +153,30 @@ def test_payload_validation_paths():
     assert lib.omo_hip_packed_Mxfp4ToFp8(None, 0, 7168, None, 0, None, 0, None) == 0
 
 
-def test_payload_pack_unpack_like_megatron():
-    """pack/unpack keep Megatron's behaviour (megatron-0.15.0rc7.diff:93-122):
-    width * 16 / 17 split, contiguous parts, its errors."""
-    from omo_python_api.ep_payload import pack_rowwise_components, payload_width, unpack_rowwise_components
+def test_payload_join_split_layout():
+    """Payload rows are [H/2 code bytes | H/32 scale bytes]: join/split
+    against byte-for-byte numpy placement, contiguous parts, shape errors."""
+    from omo_python_api.ep_payload import hidden_of, join_payload, payload_width, split_payload
     g = torch.Generator().manual_seed(3)
     q = torch.randint(0, 256, (5, 3584), generator=g, dtype=torch.uint8)
     s = torch.randint(0, 256, (5, 224), generator=g, dtype=torch.uint8)
-    p = pack_rowwise_components(q, s)
-    assert p.shape == (5, payload_width(7168)) == (5, 3808)
-    uq, us = unpack_rowwise_components(p)
+    p = join_payload(q, s)
+    assert p.shape == (5, payload_width(7168)) == (5, 3808) and hidden_of(p) == 7168
+    exp = np.zeros((5, 3808), np.uint8)
+    for t in range(5):
+        exp[t, :3584] = q[t].numpy()
+        exp[t, 3584:] = s[t].numpy()
+    np.testing.assert_array_equal(p.numpy(), exp)
+    uq, us = split_payload(p)
     assert torch.equal(uq, q) and torch.equal(us, s) and uq.is_contiguous() and us.is_contiguous()
-    with pytest.raises(ValueError, match="must match"):
-        pack_rowwise_components(q, s[:4])
-    with pytest.raises(ValueError, match="17/16"):
-        unpack_rowwise_components(torch.zeros((2, 100), dtype=torch.uint8))
-    with pytest.raises(ValueError, match="at least one dimension"):
-        unpack_rowwise_components(torch.zeros((), dtype=torch.uint8))
+    with pytest.raises(ValueError, match="tokens"):
+        join_payload(q, s[:4])
+    with pytest.raises(ValueError, match="scale bytes"):
+        join_payload(q, s[:, :200])
+    with pytest.raises(ValueError, match="17/32"):
+        split_payload(torch.zeros((2, 100), dtype=torch.uint8))
+    with pytest.raises(ValueError, match="2-D"):
+        split_payload(torch.zeros((), dtype=torch.uint8))
 
 
 def test_make_row_id_map_expert_major():

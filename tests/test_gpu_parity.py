@@ -139,15 +139,45 @@ def test_quant_parameters(oracle, dev, eps, fmin, fmax):
 
 
 def test_quant_cfg2_north_star(oracle, dev):
-    """8192 x 7168 activations with outlier channels (the benchmark input)."""
+    """8192 x 7168 activations with outlier channels (the benchmark input),
+    quantized and then dequantized back to bf16 on the GPU: codes, scale
+    bytes and the round-tripped bf16 bits all equal the oracle's."""
     import omo_workloads as wl
-    _say("quant cfg2 8192x7168")
+    _say("quant cfg2 8192x7168 + dequant back")
     x = wl.activations_with_outliers(8192, 7168, seed=2026, device="cpu")
     xb = bits_u16(x).reshape(-1)
     q, s = run_quant(xb, dev, shape=(8192, 7168))
     eq, es = oracle.quant_mxfp4(xb)
     np.testing.assert_array_equal(s, es)
     np.testing.assert_array_equal(q, eq)
+    # dequant of the GPU's own codes (equal to the oracle's, checked above)
+    np.testing.assert_array_equal(run_dequant(q, s, dev), oracle.dequant_bf16(eq, es))
+
+
+def test_cfg1_round_trip(oracle, dev):
+    """cfg1: a seeded 4096 x 4096 N(0,1) bf16 tensor quantized on the GPU
+    through the reference wrapper and dequantized back on the GPU through the
+    dequant wrapper; every stage bit-exact against the oracle."""
+    import omo_workloads as wl
+    from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
+    from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToBf16_dequant_wrapper
+    _say("cfg1 4096x4096 quant + dequant round trip")
+    x = wl.cfg1_input(device="cpu")
+    xb = bits_u16(x).reshape(-1)
+    q, s = omo_per_token_group_quant_mxfp4(x.to(dev))
+    y = omo_per_token_mxfp4ToBf16_dequant_wrapper(q, s, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert q.shape == (4096, 2048) and s.shape == (4096, 128) and y.shape == (4096, 4096)
+    eq, es = oracle.quant_mxfp4(xb)
+    np.testing.assert_array_equal(bits_u8(s).reshape(-1), es)
+    np.testing.assert_array_equal(bits_u8(q).reshape(-1), eq)
+    ey = oracle.dequant_bf16(eq, es)
+    np.testing.assert_array_equal(bits_u16(y).reshape(-1), ey)
+    # the round trip is a projection: quantizing its output reproduces it
+    q2, s2 = omo_per_token_group_quant_mxfp4(y)
+    y2 = omo_per_token_mxfp4ToBf16_dequant_wrapper(q2, s2, torch.bfloat16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits_u16(y2).reshape(-1), ey)
 
 
 @pytest.mark.parametrize("case", ["domain_tiled", "partial_last_workgroup", "steps_below_95"])
@@ -694,7 +724,7 @@ def _payload(codes, scales):
                                       (4096, 7168, 6), (4090, 7168, 7), (4096, 2048, 8), (4096, 2048, 0)])
 def test_payload_quant(oracle, dev, T, H, seed):
     """Quantize into payload rows == torch.cat of the unfused quantize outputs."""
-    from omo_python_api.ep_payload import fp4_quantize_packed, pack_rowwise_components
+    from omo_python_api.ep_payload import fp4_quantize_packed, join_payload
     from omo_python_api.mxfp4 import omo_per_token_group_quant_mxfp4
     _say("payload quant", T, H, seed)
     if seed == 0:  # the special-value blocks (inf, NaN, denormals, ...) padded to whole rows
@@ -709,7 +739,7 @@ def test_payload_quant(oracle, dev, T, H, seed):
     q, s = omo_per_token_group_quant_mxfp4(xd)
     torch.cuda.synchronize()
     assert p.shape == (T, H // 2 + H // 32) and p.dtype == torch.uint8
-    assert torch.equal(p, pack_rowwise_components(q, s))
+    assert torch.equal(p, join_payload(q, s))
     if T:
         eq, es = oracle.quant_mxfp4(bits_u16(x).reshape(-1))
         np.testing.assert_array_equal(bits_u8(p), _payload(eq.reshape(T, -1), es.reshape(T, -1)))
@@ -719,7 +749,7 @@ def test_payload_quant(oracle, dev, T, H, seed):
 def test_payload_dequant_and_requant(oracle, dev, T, H, seed, spread):
     """Dequant and FP8 requant of payload rows == the unfused kernels on the
     unpacked codes and scales (oracle), including m_splits."""
-    from omo_python_api.ep_payload import packed_mxfp4ToBf16, packed_mxfp4ToFp8, unpack_rowwise_components
+    from omo_python_api.ep_payload import packed_mxfp4ToBf16, packed_mxfp4ToFp8, split_payload
     _say("payload dequant/requant", T, H, seed, spread)
     q, s = scale_spread_payload(T, H // 2, seed, spread)
     p = torch.from_numpy(_payload(q, s)).to(dev)
@@ -728,7 +758,7 @@ def test_payload_dequant_and_requant(oracle, dev, T, H, seed, spread):
     f8s, ss = packed_mxfp4ToFp8(p, splits)
     f8, sc = packed_mxfp4ToFp8(p)
     torch.cuda.synchronize()
-    uq, us = unpack_rowwise_components(p)
+    uq, us = split_payload(p)
     assert torch.equal(uq.cpu(), torch.from_numpy(q)) and torch.equal(us.cpu(), torch.from_numpy(s))
     np.testing.assert_array_equal(bits_u16(dq).reshape(-1), oracle.dequant_bf16(q, s))
     eo, es = oracle.mxfp4_to_fp8(q, s)

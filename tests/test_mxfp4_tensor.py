@@ -150,6 +150,91 @@ def test_pickle_round_trip():
         assert s._fp8_dtype == t._fp8_dtype and s._quantizer.columnwise_usage
 
 
+class _StandInTE:
+    """Stand-ins for TE's Quantizer / QuantizedTensor / QuantizedTensorBase:
+    the constructor signatures TE's bases have, and a generic
+    __torch_dispatch__ that records which ops reach it."""
+
+    class Quantizer:
+        def __init__(self, *, rowwise: bool = True, columnwise: bool = True):
+            self.rowwise_usage, self.columnwise_usage, self.internal = rowwise, columnwise, False
+
+        def copy(self):
+            import copy
+            return copy.copy(self)
+
+        def __call__(self, tensor):
+            return self.quantize(tensor)
+
+    class QuantizedTensorBase:
+        def get_usages(self):
+            return {"rowwise": self._rowwise_data is not None, "columnwise": self._columnwise_data is not None}
+
+    class QuantizedTensor(torch.Tensor):
+        seen = []
+        result = torch.full((1,), 7.0)
+
+        def __new__(cls, shape, dtype, *, requires_grad=False, device=None):
+            return torch.Tensor._make_wrapper_subclass(cls, shape, dtype=dtype, requires_grad=requires_grad,
+                                                       device=device)
+
+        @classmethod
+        def make_like(cls, tensor, *, shape=None, dtype=None, requires_grad=False, data=None):
+            return cls(shape=tensor.shape if shape is None else shape, dtype=tensor.dtype if dtype is None else dtype,
+                       requires_grad=requires_grad, device=tensor.device, **tensor.get_metadata())
+
+        @classmethod
+        def __torch_dispatch__(cls, func, types, args, kwargs=None):
+            cls.seen.append(func)
+            return cls.result
+
+        __torch_function__ = torch._C._disabled_torch_function_impl
+
+
+def test_bind_to_te_bases():
+    """The class family rebuilt on TE-like bases: isinstance against each
+    base, the MXFP4 ops handled before the base's generic __torch_dispatch__,
+    every other op routed to it, and pickling of the bound class."""
+    mx = _mx()
+    te = _StandInTE
+    ns = mx.bind_to_te(te.Quantizer, te.QuantizedTensor, te.QuantizedTensorBase)
+    assert mx.bind_to_te(te.Quantizer, te.QuantizedTensor, te.QuantizedTensorBase) is ns
+    q = ns.MXFP4Quantizer(rowwise=True, columnwise=True)
+    assert isinstance(q, te.Quantizer) and not isinstance(q, mx.Quantizer)
+    t = q.make_empty((256, 64), dtype=torch.bfloat16, device="cpu")
+    assert type(t) is ns.MXFP4Tensor and type(t).__name__ == "TEMXFP4Tensor"
+    assert isinstance(t, te.QuantizedTensor) and isinstance(t, te.QuantizedTensorBase)
+    assert isinstance(t, ns.MXFP4TensorBase) and not isinstance(t, mx.MXFP4Tensor)
+    assert t.get_usages() == {"rowwise": True, "columnwise": True}
+    assert t._rowwise_data.shape == (256, 32) and t._columnwise_data.shape == (64, 128)
+    e = torch.empty_like(t)                                # handled by MXFP4Tensor
+    assert type(e) is ns.MXFP4Tensor and e._columnwise_scale_inv.shape == t._columnwise_scale_inv.shape
+    assert t.zero_() is t and int(t._rowwise_data.count_nonzero()) == 0
+    assert type(t.detach()) is ns.MXFP4Tensor
+    te.QuantizedTensor.seen.clear()
+    assert torch.ops.aten.add.Tensor(t, t) is te.QuantizedTensor.result  # anything else goes to the base
+    assert te.QuantizedTensor.seen == [torch.ops.aten.add.Tensor]
+    tensors, obj = t.prepare_for_saving()
+    assert obj is t and len(tensors) == 4 and t._rowwise_data is None
+    t.restore_from_saved(tensors + ["rest"])
+    s = pickle.loads(pickle.dumps(t))
+    assert type(s) is ns.MXFP4Tensor and torch.equal(s._rowwise_data, t._rowwise_data)
+    # the module's default family is untouched
+    assert not isinstance(mx.MXFP4Quantizer(), te.Quantizer)
+
+
+def test_bind_to_te_without_te():
+    """With no bases given the TE package is imported; it is absent here."""
+    mx = _mx()
+    try:
+        import transformer_engine  # noqa: F401
+        pytest.skip("transformer_engine is installed")
+    except ImportError:
+        pass
+    with pytest.raises(ImportError):
+        mx.bind_to_te()
+
+
 def _torch_save_load(t):
     buf = io.BytesIO()
     torch.save(t, buf)
