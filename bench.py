@@ -309,8 +309,14 @@ def main():
         with open(tpath) as f:
             tj = json.load(f)
         traffic = tj.get("hbm_bytes_per_launch")
+        import hashlib
+        srcs = tj.get("sources_sha256") or {}
+        current = {f: hashlib.sha256(open(os.path.join(ROOT, f), "rb").read()).hexdigest()
+                   for f in srcs if os.path.exists(os.path.join(ROOT, f))}
         traffic_source = {"file": "profiles/traffic_quant_phased_cfg2.json",
-                          **{k: tj.get(k) for k in ("measured_at_commit", "library_sha256_16", "command")}}
+                          "measured_at_commit": tj.get("measured_at_commit"),
+                          "method": "median TCC read/write request bytes per dispatch (rocprofv3 --pmc)",
+                          "kernel_sources_unchanged": bool(srcs) and current == srcs}
 
     # ---- extra legs -------------------------------------------------------
     if want("dequant"):
