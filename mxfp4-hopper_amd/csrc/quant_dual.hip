@@ -198,39 +198,67 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
 // ---- four tiles per workgroup, for M % 64 == 0 and K % 256 == 0
 //
 // A workgroup quantizes the (up to) four vertically adjacent 64 x 256 tiles
-// of a 256-row super-tile one after the other, as dual_tile does, but keeps
+// of a 256-row super-tile one after the other, as dual_tile does, and keeps
 // each lane's transposed-code pieces (8 B per column and tile) and column
-// scale pairs in registers. After the last tile the four lanes of a column
-// pair (bands b = 0..3) transpose their 4 x 4 pieces (two DPP butterflies),
-// so lane b holds tile b's 32 B of each of its two columns and writes them
-// as two 16 B stores: a column's 128 B line takes two store requests instead
-// of four, and its 8 scale bytes one 8-byte store instead of four 2-byte
-// ones (a CU issues one request per cache line a store instruction touches).
+// scale pairs in registers. After the last tile the pieces are staged in LDS
+// (the tile buffer, now free) and leave as whole 128 B column lines, eight
+// lanes per line in one store instruction, and each column's 8 scale bytes
+// as one 8-byte store. A tile's rowwise codes and scale bytes are staged in
+// LDS too and stored one tile later, after that tile's loads were consumed:
+// loads and stores share one vector-memory counter, so a store issued just
+// ahead of a load makes the wait for that load wait for the store as well.
+// Memory-only copies of this schedule (the same loads and stores, no
+// arithmetic) run within 1-2 us of the kernel: its time is set by the mix of
+// the strided 512 B row reads with the 128 B code lines and the 8-byte scale
+// pieces, whose lines other workgroups complete.
 constexpr int kSuperSteps = 4;
 constexpr int kSuperRows = kDualRows * kSuperSteps;  // 256
 
-__device__ __forceinline__ uint2 dpp_quad_xor2_u2(uint2 v) { return make_uint2(dpp_quad_xor2(v.x), dpp_quad_xor2(v.y)); }
-__device__ __forceinline__ uint2 dpp_quad_xor1_u2(uint2 v) { return make_uint2(dpp_quad_xor1(v.x), dpp_quad_xor1(v.y)); }
+struct DualSuperSmem {
+  // the staged 64 x 256 input tile; after a super-tile's last tile, its
+  // transposed codes [256 columns][128 B] (16 B pieces XOR-swizzled by column)
+  __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
+  __attribute__((aligned(16))) uint32_t row_codes[2][kDualRows * kDualCols / 8];  // by tile parity
+  __attribute__((aligned(8))) uint8_t row_scales[2][kDualRows * 8];
+};
 
-// Lane b (of a quad) holds e[s] = piece (b, s); afterwards e[s] = piece (s, b).
-__device__ __forceinline__ void quad_transpose4(uint2 (&e)[4], int b) {
-  uint2 o[4];
-#pragma unroll
-  for (int s = 0; s < 4; s++) o[s] = dpp_quad_xor2_u2(e[s ^ 2]);  // lane b ^ 2's piece s ^ 2
-#pragma unroll
-  for (int s = 0; s < 4; s++)
-    if ((s & 2) != (b & 2)) e[s] = o[s];
-#pragma unroll
-  for (int s = 0; s < 4; s++) o[s] = dpp_quad_xor1_u2(e[s ^ 1]);  // lane b ^ 1's piece s ^ 1
-#pragma unroll
-  for (int s = 0; s < 4; s++)
-    if ((s & 1) != (b & 1)) e[s] = o[s];
+// threadIdx.x through an empty asm statement: address arithmetic built on it
+// is recomputed where it is used instead of being hoisted out of the loop and
+// held in registers for the whole kernel.
+__device__ __forceinline__ int opaque_tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// Byte offset of transposed-code byte `b` (0..127) of column c in the staging area.
+__device__ __forceinline__ int col_stage_off(int c, int b) { return c * 128 + ((((b >> 4) ^ c) & 7) << 4) + (b & 15); }
+
+// Rowwise codes and scale bytes of one tile (64 rows from m0), staged in
+// buffer `buf`: each lane stores 16 code bytes (8 lanes per 128 B line of a
+// row) and lanes 0..63 one row's 8 scale bytes.
+__device__ __forceinline__ void dual_row_flush(const DualSuperSmem& sm, int buf, uint32_t* __restrict__ row_q,
+                                               uint8_t* __restrict__ row_s, int64_t m0, int64_t k0, int64_t K,
+                                               bool rs_vec) {
+  const int t = threadIdx.x;
+  const int row = t >> 3, piece = t & 7;
+  const u32x4 c = *reinterpret_cast<const u32x4*>(&sm.row_codes[buf][row * (kDualCols / 8) + 4 * piece]);
+  __builtin_nontemporal_store(c, reinterpret_cast<u32x4*>(row_q + (m0 + row) * (K / 8) + k0 / 8 + 4 * piece));
+  if (t < kDualRows) {
+    uint8_t* rs = row_s + (m0 + t) * (K / 32) + k0 / 32;
+    const uint2 v = *reinterpret_cast<const uint2*>(&sm.row_scales[buf][t * 8]);
+    if (rs_vec) {
+      *reinterpret_cast<uint2*>(rs) = v;
+    } else {
+      for (int j = 0; j < 8; j++) rs[j] = (uint8_t)((j < 4 ? v.x : v.y) >> (8 * (j & 3)));
+    }
+  }
 }
 
 __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
                                             uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
                                             uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms,
-                                            int logical, float eps, int c_eps, uint8_t* tile, uint8_t* rs_tile) {
+                                            int logical, float eps, int c_eps, DualSuperSmem& sm) {
   const int t = threadIdx.x;
   const int64_t m0s = (int64_t)(logical % tiles_ms) * kSuperRows, k0 = (int64_t)(logical / tiles_ms) * kDualCols;
   const int steps = (int)((M - m0s) / kDualRows < kSuperSteps ? (M - m0s) / kDualRows : kSuperSteps);
@@ -247,14 +275,14 @@ __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint
   uint32_t sc_lo = 0, sc_hi = 0;  // scale pairs of column kc + g, tile s at bytes 2s, 2s + 1
   for (int st = 0; st < steps; st++) {
     const int64_t m0 = m0s + st * kDualRows;
+    const int buf = st & 1;
     const uint16_t* src = x + (m0 + r0) * K + k0 + cc * 8;
     u32x4 d[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) d[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16 * k * K));
-    uint32_t* rq = row_q + (m0 + r0) * (K / 8) + k0 / 8 + cc;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      *reinterpret_cast<u32x4*>(tile + (r0 + 16 * k) * kDualPitch + ((cc ^ (k << 2)) * 16)) = d[k];
+      *reinterpret_cast<u32x4*>(sm.tile + (r0 + 16 * k) * kDualPitch + ((cc ^ (k << 2)) * 16)) = d[k];
       uint32_t codes, byte;
       const uint32_t am = quad_max_u32(chunk_absmax_bits(d[k]));
       if (__builtin_expect(am < 0x7F80u, 1)) {
@@ -262,24 +290,17 @@ __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint
       } else {
         quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
       }
-      __builtin_nontemporal_store(codes, rq + k * 2 * K);
-      if (quad_leader) rs_tile[(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)byte;
+      sm.row_codes[buf][(r0 + 16 * k) * (kDualCols / 8) + cc] = codes;
+      if (quad_leader) sm.row_scales[buf][(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)byte;
     }
+    if (st > 0) dual_row_flush(sm, buf ^ 1, row_q, row_s, m0 - kDualRows, k0, K, rs_vec);
     __syncthreads();
-    if (t < kDualRows) {
-      uint8_t* rs = row_s + (m0 + t) * (K / 32) + k0 / 32;
-      if (rs_vec) {
-        *reinterpret_cast<uint2*>(rs) = *reinterpret_cast<const uint2*>(rs_tile + t * 8);
-      } else {
-        for (int j = 0; j < 8; j++) rs[j] = rs_tile[t * 8 + j];
-      }
-    }
     uint32_t ca[8], cb[8];
     uint32_t amax_a = 0, amax_b = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const uint32_t w0 = *reinterpret_cast<const uint32_t*>(tile + (16 * band + 2 * j) * kDualPitch + pp);
-      const uint32_t w1 = *reinterpret_cast<const uint32_t*>(tile + (16 * band + 2 * j + 1) * kDualPitch + pp);
+      const uint32_t w0 = *reinterpret_cast<const uint32_t*>(sm.tile + (16 * band + 2 * j) * kDualPitch + pp);
+      const uint32_t w1 = *reinterpret_cast<const uint32_t*>(sm.tile + (16 * band + 2 * j + 1) * kDualPitch + pp);
       ca[j] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
       cb[j] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
       amax_a = pk_max_u16(amax_a, ca[j] & 0x7FFF7FFFu);
@@ -308,15 +329,28 @@ __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint
     else sc_hi |= pair << (16 * (st - 2));
     __syncthreads();  // this tile's LDS reads are done before the next tile's writes
   }
-  quad_transpose4(acc_a, band);
-  quad_transpose4(acc_b, band);
-  if (band < steps) {  // lane b: tile b's 32 B of columns kc and kc + 1
-    uint8_t* da = col_q + kc * (M / 2) + m0s / 2 + 32 * band;
-    uint8_t* db = da + M / 2;
-    *reinterpret_cast<u32x4*>(da) = u32x4{acc_a[0].x, acc_a[0].y, acc_a[1].x, acc_a[1].y};
-    *reinterpret_cast<u32x4*>(da + 16) = u32x4{acc_a[2].x, acc_a[2].y, acc_a[3].x, acc_a[3].y};
-    *reinterpret_cast<u32x4*>(db) = u32x4{acc_b[0].x, acc_b[0].y, acc_b[1].x, acc_b[1].y};
-    *reinterpret_cast<u32x4*>(db + 16) = u32x4{acc_b[2].x, acc_b[2].y, acc_b[3].x, acc_b[3].y};
+  dual_row_flush(sm, (steps - 1) & 1, row_q, row_s, m0s + (int64_t)(steps - 1) * kDualRows, k0, K, rs_vec);
+  {
+    const int tt = opaque_tid(), pl = tt >> 2, bl = tt & 3;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      if (s < steps) {
+        *reinterpret_cast<uint2*>(sm.tile + col_stage_off(2 * pl, 32 * s + 8 * bl)) = acc_a[s];
+        *reinterpret_cast<uint2*>(sm.tile + col_stage_off(2 * pl + 1, 32 * s + 8 * bl)) = acc_b[s];
+      }
+    }
+  }
+  __syncthreads();
+  {
+    const int tc = opaque_tid();
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int c = (tc >> 3) + 64 * j, piece = tc & 7;
+      if (piece < 2 * steps) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(sm.tile + col_stage_off(c, 16 * piece));
+        *reinterpret_cast<u32x4*>(col_q + (k0 + c) * (M / 2) + m0s / 2 + 16 * piece) = v;
+      }
+    }
   }
   if (h == 0) {  // lane g: column kc + g's scale bytes of the super-tile
     uint8_t* cs = col_s + (kc + g) * (M / 32) + m0s / 32;
@@ -328,16 +362,18 @@ __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint
   }
 }
 
-__global__ __launch_bounds__(kDualThreads) void quant_dual_super_kernel(
+// At most 80 VGPRs (six waves per SIMD): three 512-thread workgroups per CU,
+// which the LDS (52 KB each) also allows; at 86 the compiler's own choice,
+// two fit and the kernel ran 8% slower.
+__global__ __launch_bounds__(kDualThreads) __attribute__((amdgpu_waves_per_eu(6))) void quant_dual_super_kernel(
     const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q, uint8_t* __restrict__ row_s,
     uint8_t* __restrict__ col_q, uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms, int tiles,
     int per_xcd, float eps, int c_eps) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
-  __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
+  __shared__ DualSuperSmem sm;
   const int b = blockIdx.x;
   const int logical = (b % kXcds) * per_xcd + b / kXcds;
   if (logical >= tiles) return;
-  dual_super4(x, row_q, row_s, col_q, col_s, M, K, tiles_ms, logical, eps, c_eps, tile, rs_tile);
+  dual_super4(x, row_q, row_s, col_q, col_s, M, K, tiles_ms, logical, eps, c_eps, sm);
 }
 
 __global__ __launch_bounds__(kDualThreads) void quant_dual_kernel(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
@@ -387,9 +423,9 @@ __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const 
 
 // Grouped form of quant_dual_super_kernel: every item has M % 64 == 0,
 // K % 256 == 0 and aligned buffers; tiles_m and tile_begin count super-tiles.
-__global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_super_kernel(const DualGroup g) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
-  __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
+__global__ __launch_bounds__(kDualThreads) __attribute__((amdgpu_waves_per_eu(6))) void quant_dual_grouped_super_kernel(
+    const DualGroup g) {
+  __shared__ DualSuperSmem sm;
   const int b = blockIdx.x;
   const int logical = (b % kXcds) * g.per_xcd + b / kXcds;
   if (logical >= g.tiles) return;
@@ -397,14 +433,14 @@ __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_super_kernel(
   while (i + 1 < g.count && logical >= g.item[i + 1].tile_begin) i++;
   const DualItem& it = g.item[i];
   dual_super4(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, it.tiles_m, logical - it.tile_begin, g.eps,
-              g.c_eps, tile, rs_tile);
+              g.c_eps, sm);
 }
 
 // Shapes and buffers the four-tile kernels take: whole 64 x 256 tiles, 16 B
-// aligned input and transposed codes, dword-aligned rowwise codes.
+// aligned input, rowwise codes and transposed codes.
 static bool dual_super_ok(const void* x, const void* row_q, const void* col_q, int64_t M, int64_t K) {
   return M % kDualRows == 0 && K % kDualCols == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
-         (reinterpret_cast<uintptr_t>(row_q) & 3) == 0 && (reinterpret_cast<uintptr_t>(col_q) & 15) == 0;
+         (reinterpret_cast<uintptr_t>(row_q) & 15) == 0 && (reinterpret_cast<uintptr_t>(col_q) & 15) == 0;
 }
 
 hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_q, void* col_s, int64_t M, int64_t K,
