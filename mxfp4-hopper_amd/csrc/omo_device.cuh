@@ -154,6 +154,15 @@ __device__ __forceinline__ uint32_t xcd_contiguous(uint32_t b, uint32_t n) {
   return x * q + (x < r ? x : r) + j;
 }
 
+// threadIdx.x through an empty asm statement: address arithmetic built on it
+// is recomputed where it is used instead of being hoisted out of the loop and
+// held in registers for the whole kernel.
+__device__ __forceinline__ int opaque_tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // Exact ceil(log2(z)) for a finite normal float z > 0.
 __device__ __forceinline__ int ceil_log2_normal(float z) {
   uint32_t b = __float_as_uint(z);

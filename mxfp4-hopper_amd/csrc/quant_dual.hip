@@ -222,15 +222,6 @@ struct DualSuperSmem {
   __attribute__((aligned(8))) uint8_t row_scales[2][kDualRows * 8];
 };
 
-// threadIdx.x through an empty asm statement: address arithmetic built on it
-// is recomputed where it is used instead of being hoisted out of the loop and
-// held in registers for the whole kernel.
-__device__ __forceinline__ int opaque_tid() {
-  int t = (int)threadIdx.x;
-  asm volatile("" : "+v"(t));
-  return t;
-}
-
 // Byte offset of transposed-code byte `b` (0..127) of column c in the staging area.
 __device__ __forceinline__ int col_stage_off(int c, int b) { return c * 128 + ((((b >> 4) ^ c) & 7) << 4) + (b & 15); }
 

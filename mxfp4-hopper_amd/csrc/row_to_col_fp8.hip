@@ -59,6 +59,35 @@ __device__ __forceinline__ float oct_fmax(float v) {
   return fmaxf(v, o);
 }
 
+// oct_fmax for values that are all >= 0 (not NaN): such floats are ordered as
+// their bit patterns are as signed integers, so the maximum is an integer
+// maximum, which needs none of the NaN quieting that fmaxf costs (two more
+// instructions per step) and folds into DPP forms.
+__device__ __forceinline__ float oct_max_nonneg(float v) {
+  int x = __float_as_int(v);
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true));   // quad_perm [1,0,3,2]
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true));   // quad_perm [2,3,0,1]
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true));  // row_half_mirror
+  return __int_as_float(x);
+}
+
+// Column maxima of n values per lane reduced over 8-lane groups: the integer
+// form when every lane of the wave holds values >= 0 (the usual case: the
+// maxima start from 0 or eps and take |v|), else fmaxf.
+template <int n>
+__device__ __forceinline__ void oct_max_all(float (&a)[n]) {
+  bool nonneg = true;
+#pragma unroll
+  for (int e = 0; e < n; e++) nonneg = nonneg && a[e] >= 0.0f;  // false for NaN
+  if (__builtin_amdgcn_ballot_w64(!nonneg) == 0) {
+#pragma unroll
+    for (int e = 0; e < n; e++) a[e] = oct_max_nonneg(a[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < n; e++) a[e] = oct_fmax(a[e]);
+  }
+}
+
 struct RowColSmem {
   uint8_t codes[kTile * kCodePitch];
   uint32_t fscales[4][kTile];  // s << 23: the fp32 pattern of 2^(s-127), [MX block of the tile][row]
@@ -243,8 +272,12 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
       a1 = fmaxf(a1, fabsf(v1));
     }
   }
-  a0 = oct_fmax(a0);
-  a1 = oct_fmax(a1);
+  {
+    float am[2] = {a0, a1};
+    oct_max_all(am);
+    a0 = am[0];
+    a1 = am[1];
+  }
   float m0, m1, inv0, inv1;
   rc_factors<MSPLIT>(a0, a1, eps, &m0, &m1, &inv0, &inv1);
   if (qq == 0 && col_valid) {
@@ -428,9 +461,11 @@ struct WideSmem {
   uint8_t scales[8][kTile];
 };
 
-// The column-maximum pass converts with volatile asm, so the compiler does not
-// keep its 128 values per lane alive for the output pass (which converts
-// again) and spill them.
+// The output pass converts with volatile asm, so the compiler neither keeps
+// the column-maximum pass's 128 values per lane alive for it (it converts
+// again) nor hoists its conversions above the clamp branch, and spills none
+// of them. The column-maximum pass uses the builtin, which the compiler
+// schedules around the conversion's latency.
 template <int B>
 __device__ __forceinline__ void cvt_pk_f32_fp4_once(uint32_t src, float scale, float* lo, float* hi) {
   typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -448,7 +483,7 @@ __device__ __forceinline__ void wide_amax_fast(const uint32_t (&cw)[16], const f
 #pragma unroll
   for (int j = 0; j < 16; j++) {
     float v0, v1;
-    cvt_pk_f32_fp4_once<B>(cw[j], sc[j], &v0, &v1);
+    cvt_pk_f32_fp4<B>(cw[j], sc[j], &v0, &v1);
     a[2 * B] = fmaxf(a[2 * B], fabsf(v0));
     a[2 * B + 1] = fmaxf(a[2 * B + 1], fabsf(v1));
   }
@@ -464,12 +499,37 @@ __device__ __forceinline__ void wide_pair_fast(const uint32_t (&cw)[16], const f
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       float v0, v1;
-      cvt_pk_f32_fp4<B>(cw[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
+      cvt_pk_f32_fp4_once<B>(cw[4 * j4 + k], sc[4 * j4 + k], &v0, &v1);
       x[k] = CLAMP ? __builtin_amdgcn_fmed3f(v0 * m0, -448.0f, 448.0f) : v0 * m0;
       y[k] = CLAMP ? __builtin_amdgcn_fmed3f(v1 * m1, -448.0f, 448.0f) : v1 * m1;
     }
     w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
     w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+  }
+}
+
+// Per split, no clamp: the multiplier of a column is 1 / inv with inv = 2^k,
+// and v_cvt_scalef32_pk_fp8_f32 (x, y, inv) gives the bytes of
+// v_cvt_pk_fp8_f32 (x / inv, y / inv) = v_cvt_pk_fp8_f32 (x * m, y * m)
+// (checked equal on the GPU for every finite 2^k, k = -126 .. 127, over all
+// E2M1 magnitudes times 2^e and random inputs), one instruction per two
+// values instead of three.
+template <int B>
+__device__ __forceinline__ void wide_pair_scaled(const uint32_t (&cw)[16], const float (&sc)[16], float inv0,
+                                                 float inv1, u32x4& w0, u32x4& w1) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int j4 = 0; j4 < 4; j4++) {
+    float x[4], y[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) cvt_pk_f32_fp4_once<B>(cw[4 * j4 + k], sc[4 * j4 + k], &x[k], &y[k]);
+    const s16x2 z = {0, 0};
+    const s16x2 a = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(
+        __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(z, x[0], x[1], inv0, false), x[2], x[3], inv0, true);
+    const s16x2 b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(
+        __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(z, y[0], y[1], inv1, false), y[2], y[3], inv1, true);
+    w0[j4] = (uint32_t)(uint16_t)a[0] | ((uint32_t)(uint16_t)a[1] << 16);
+    w1[j4] = (uint32_t)(uint16_t)b[0] | ((uint32_t)(uint16_t)b[1] << 16);
   }
 }
 
@@ -512,8 +572,7 @@ __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, co
       for (int e = 0; e < 8; e++) a[e] = fmaxf(a[e], fabsf(bf16_to_f32(e2m1_to_bf16_bits((cw[j] >> (4 * e)) & 0xFu)) * s16));
     }
   }
-#pragma unroll
-  for (int e = 0; e < 8; e++) a[e] = oct_fmax(a[e]);
+  oct_max_all(a);
   float ae = a[0];
 #pragma unroll
   for (int e = 1; e < 8; e++) ae = qq == e ? a[e] : ae;
@@ -528,9 +587,13 @@ __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, co
   }
   if (store_s) __builtin_nontemporal_store(iown, out_s_lane);
   const int base = (int)(threadIdx.x & 63) & ~7;
-  float m[8];
+  float m[8], iv[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) m[e] = lane_value(mown, base + e);
+  if (MSPLIT) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) iv[e] = lane_value(iown, base + e);
+  }
   // The clamp to +-448 is left out where it changes no byte, as in rc_tile:
   // always for the dense kernel; per split where every column has amax > eps
   // or amax <= 448 (and finite multipliers).
@@ -538,13 +601,27 @@ __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, co
   if (MSPLIT) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      finite_m = finite_m && m[e] < __builtin_inff();
+      // multiplier and scale finite (the scaled conversion divides by inv)
+      finite_m = finite_m && m[e] < __builtin_inff() && iv[e] < __builtin_inff();
       no_clamp = no_clamp && (a[e] > eps || a[e] <= 448.0f);
     }
   }
   if (fast && finite_m) {
     u32x4 w0, w1;
-    if (no_clamp) {
+    if (MSPLIT && no_clamp) {
+      wide_pair_scaled<0>(cw, sc, iv[0], iv[1], w0, w1);
+      put(0, w0);
+      put(1, w1);
+      wide_pair_scaled<1>(cw, sc, iv[2], iv[3], w0, w1);
+      put(2, w0);
+      put(3, w1);
+      wide_pair_scaled<2>(cw, sc, iv[4], iv[5], w0, w1);
+      put(4, w0);
+      put(5, w1);
+      wide_pair_scaled<3>(cw, sc, iv[6], iv[7], w0, w1);
+      put(6, w0);
+      put(7, w1);
+    } else if (no_clamp) {
       wide_pair_fast<0, false>(cw, sc, m[0], m[1], w0, w1);
       put(0, w0);
       put(1, w1);

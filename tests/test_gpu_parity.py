@@ -471,6 +471,33 @@ def test_row_to_fp8_col_wide_scales(oracle, dev):
     np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
+@pytest.mark.parametrize("N", [512, 384])
+@pytest.mark.parametrize("eps", [-1.0, -0.0, 1e-10])
+def test_row_to_fp8_col_nan_lane_groups(oracle, dev, N, eps):
+    """Lanes whose values are all NaN: codes 0 with scale byte 255 (0 * inf)
+    over whole 16-row lane groups, so that with eps negative a lane's column
+    maximum stays eps (< 0) and the kernels reduce the maxima with fmaxf
+    rather than as integers; eps -0.0 keeps -0.0 maxima. N = 512 takes the
+    256-column tiles, N = 384 the 128-column ones."""
+    _say("row_to_fp8_col nan lane groups", N, eps)
+    omo = _omo()
+    rng = np.random.default_rng(N)
+    M = 256
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(100, 140, size=(M, N // 32)).astype(np.uint8)
+    q[16:32, 0:16] = 0      # rows 16..31, element columns 0..31: codes 0
+    s[16:32, 0] = 255       # ... with scale 2^128 (inf): every value NaN
+    q[128:256, 32:48] = 0   # a whole tile's rows for element columns 64..95
+    s[128:256, 2] = 255
+    out = torch.empty((N, M), dtype=FP8, device=dev)
+    outs = torch.empty((M // 128, N), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, eps)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s, eps=eps)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
 @pytest.mark.parametrize("lo,hi", [(1, 4), (250, 254), (1, 252), (0, 3)])
 def test_row_to_fp8_col_scale_edges(oracle, dev, lo, hi):
     """Scale bytes at the ends of the range: subnormal products (1..4), the
