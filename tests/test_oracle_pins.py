@@ -314,6 +314,102 @@ def test_msplit_numpy_restatement(oracle):
         soff += (m + 127) // 128
 
 
+def fp8_values(codes):
+    """E4M3 bytes -> float64 values (torch's float8_e4m3fn decode)."""
+    return torch.from_numpy(np.ascontiguousarray(codes)).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+
+
+def _check_fp8_columns(V, out_cols, scale_row, maxima_hit):
+    """Properties of one tile's FP8 columns that any correct conversion has:
+    q * scale reproduces every value to half an E4M3 step (2^-4 relative, or
+    2^-10 * scale below the normal range), and each column's largest |v|
+    lands on the FP8 values maxima_hit allows."""
+    tile = V.astype(np.float64)
+    q = fp8_values(out_cols).T  # [rows, cols]
+    sc = scale_row.astype(np.float64)[None, :]
+    err = np.abs(q * sc - tile)
+    bound = 2.0 ** -4 * np.abs(tile) + 2.0 ** -10 * sc + 1e-6 * np.abs(tile)
+    assert np.all(err <= bound)
+    amax = np.abs(tile).max(axis=0)
+    for c in range(tile.shape[1]):
+        r = int(np.argmax(np.abs(tile[:, c])))
+        if amax[c] > 0:
+            assert maxima_hit(abs(q[r, c]))
+
+
+def test_row_to_fp8_col_properties(oracle):
+    """The dense conversion against properties rather than its formula:
+    per-tile error bound and column maxima at +-448; rows permuted inside a
+    128-row tile permute the output columns the same way; a column's codes
+    change only that column's output; every scale byte + k keeps the FP8
+    bytes and multiplies the column scales by exactly 2^k."""
+    rng = np.random.default_rng(31)
+    M, N = 256, 256
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(100, 140, size=(M, N // 32)).astype(np.uint8)
+    out, outs = oracle.row_to_fp8_col(q, s)
+    V = dequant_matrix(q, s, N)
+    for t in range(M // 128):
+        _check_fp8_columns(V[t * 128:(t + 1) * 128], out[:, t * 128:(t + 1) * 128], outs[t],
+                           lambda a: a == 448.0)
+    perm = np.concatenate([rng.permutation(128), 128 + rng.permutation(128)])
+    outp, outsp = oracle.row_to_fp8_col(q[perm], s[perm])
+    np.testing.assert_array_equal(outp, out[:, perm])
+    np.testing.assert_array_equal(outsp.view(np.uint32), outs.view(np.uint32))
+    q2 = q.copy()
+    q2[:128, 5] = rng.integers(0, 256, size=128, dtype=np.uint8)  # element columns 10 and 11, first tile
+    out2, outs2 = oracle.row_to_fp8_col(q2, s)
+    changed = np.any(out2 != out, axis=1) | np.any(outs2.view(np.uint32) != outs.view(np.uint32), axis=0)
+    assert set(np.nonzero(changed)[0]) <= {10, 11}
+    np.testing.assert_array_equal(out2[:, 128:], out[:, 128:])
+    out3, outs3 = oracle.row_to_fp8_col(q, s + 7)
+    np.testing.assert_array_equal(out3, out)
+    np.testing.assert_array_equal(outs3, (outs.astype(np.float64) * 2.0 ** 7).astype(np.float32))
+
+
+def test_msplit_properties(oracle):
+    """The per-split conversion against properties: a split converted alone
+    gives the same bytes as its block of the joint output (the layout off*N +
+    c*len, tiles from the split's own start); scales are the smallest power of
+    two at or above fl(amax/448); the error bound per element; column maxima
+    land in (224, 448]; scale bytes + k keep the bytes and multiply the scales
+    by 2^k."""
+    rng = np.random.default_rng(32)
+    splits = [129, 1, 256, 200]
+    M, N = sum(splits), 256
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(100, 140, size=(M, N // 32)).astype(np.uint8)
+    out, outs = oracle.row_to_fp8_col_msplit(q, s, splits)
+    V = dequant_matrix(q, s, N)
+    off = soff = 0
+    for m in splits:
+        alone, alone_s = oracle.row_to_fp8_col_msplit(q[off:off + m], s[off:off + m], [m])
+        np.testing.assert_array_equal(out[off * N:(off + m) * N], alone)
+        np.testing.assert_array_equal(outs[soff:soff + (m + 127) // 128].view(np.uint32), alone_s.view(np.uint32))
+        blk = out[off * N:(off + m) * N].reshape(N, m)
+        for t in range((m + 127) // 128):
+            tile = V[off + t * 128: off + min(m, (t + 1) * 128)]
+            sc = outs[soff + t].astype(np.float64)
+            amax = np.abs(tile).max(axis=0)
+            lower = (amax / np.float32(448)).astype(np.float32).astype(np.float64)
+            assert np.all(np.log2(sc) == np.round(np.log2(sc)))  # powers of two
+            big = amax > 1e-10  # the wrapper's eps; at or below it the scale is 1
+            assert np.all((sc[big] >= lower[big]) & (sc[big] < 2 * lower[big])) and np.all(sc[~big] == 1.0)
+            _check_fp8_columns(tile, blk[:, t * 128: t * 128 + tile.shape[0]], outs[soff + t],
+                               lambda a: 224.0 < a <= 448.0)
+        off += m
+        soff += (m + 127) // 128
+    # scale bytes + 5: the same bytes; every scale doubled five times except
+    # those of all-zero columns (amax 0 <= eps: scale 1 either way)
+    out3, outs3 = oracle.row_to_fp8_col_msplit(q, s + 5, splits)
+    np.testing.assert_array_equal(out3, out)
+    zero = np.concatenate([[np.abs(V[o + t * 128: o + min(m, (t + 1) * 128)]).max(axis=0) == 0
+                            for t in range((m + 127) // 128)]
+                           for o, m in zip(np.cumsum([0] + splits[:-1]), splits)])
+    expect = np.where(zero, outs, (outs.astype(np.float64) * 2.0 ** 5).astype(np.float32))
+    np.testing.assert_array_equal(outs3, expect)
+
+
 def test_te_pow2_scale_known_answers(oracle):
     assert oracle.te_pow2_scale(448.0) == 1.0
     assert oracle.te_pow2_scale(449.0) == 0.5
