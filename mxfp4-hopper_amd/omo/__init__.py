@@ -265,7 +265,6 @@ def omo_quant_mxfp4_dual(input, row_q, row_s, col_q, col_s, eps=1e-10):
             row_s.numel(), col_q.data_ptr(), col_q.numel(), col_s.data_ptr(), col_s.numel(), float(eps), stream))
 
 
-
 def omo_quant_mxfp4_dual_grouped(inputs, outputs, eps=1e-10):
     """omo_quant_mxfp4_dual over a list of 2-D bf16 tensors in one launch (per
     32 tensors). outputs[i] = (row_q, row_s, col_q, col_s) of inputs[i]."""
