@@ -35,6 +35,17 @@ int from_hip(hipError_t e, const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// Products of caller-supplied sizes go through size_mul: a * b for a, b >= 0,
+// or -1 when it passes 2^60 (beyond any device's memory, and far enough below
+// 2^63 that the small multiples taken of it afterwards stay exact).
+constexpr int64_t kMaxSize = (int64_t)1 << 60;
+
+int64_t size_mul(int64_t a, int64_t b) {
+  int64_t r;
+  if (a < 0 || b < 0 || __builtin_mul_overflow(a, b, &r) || r > kMaxSize) return -1;
+  return r;
+}
+
 #define REQUIRE(cond, ...)                                  \
   do {                                                      \
     if (!(cond)) return fail(OMO_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
@@ -54,6 +65,7 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 int check_requant_common(const char* fn, const void* input, int64_t rows, int64_t row_bytes, int scale_ue8m0) {
   REQUIRE(rows >= 0 && row_bytes >= 0, "%s: negative shape", fn);
   if (scale_ue8m0) return fail(OMO_ERR_UNSUPPORTED, "%s: scale_ue8m0 is not supported (the reference asserts it off)", fn);
+  REQUIRE(size_mul(rows, row_bytes) >= 0, "%s: shape too large", fn);
   REQUIRE(rows * row_bytes % 128 == 0, "%s: input.numel() %% 128 != 0 (input.numel()=%lld)", fn,
           (long long)(rows * row_bytes));
   (void)input;
@@ -97,9 +109,13 @@ int check_permute(const char* fn, const void* codes, int64_t codes_bytes, int64_
   REQUIRE(num_tokens >= 0 && cols >= 0 && num_out >= 0, "%s: negative shape", fn);
   REQUIRE(cols % 32 == 0, "%s: cols must be a multiple of 32 (got %lld)", fn, (long long)cols);
   REQUIRE(num_tokens < ((int64_t)1 << 31) && num_out < ((int64_t)1 << 31), "%s: too many rows", fn);
+  REQUIRE(cols <= kMaxSize && code_stride <= kMaxSize && scale_stride <= kMaxSize, "%s: shape too large", fn);
   REQUIRE(code_stride >= cols / 2 && scale_stride >= cols / 32, "%s: row stride shorter than the row", fn);
-  const int64_t code_need = num_tokens == 0 ? 0 : (num_tokens - 1) * code_stride + cols / 2;
-  const int64_t scale_need = num_tokens == 0 ? 0 : (num_tokens - 1) * scale_stride + cols / 32;
+  const int64_t code_span = num_tokens == 0 ? 0 : size_mul(num_tokens - 1, code_stride);
+  const int64_t scale_span = num_tokens == 0 ? 0 : size_mul(num_tokens - 1, scale_stride);
+  REQUIRE(code_span >= 0 && scale_span >= 0 && size_mul(num_out, cols) >= 0, "%s: shape too large", fn);
+  const int64_t code_need = num_tokens == 0 ? 0 : code_span + cols / 2;
+  const int64_t scale_need = num_tokens == 0 ? 0 : scale_span + cols / 32;
   REQUIRE_BUF("codes", codes, codes_bytes, code_need);
   REQUIRE_BUF("scales", scales, scales_bytes, scale_need);
   REQUIRE(num_out == 0 || src_rows != nullptr, "%s: src_rows: null pointer", fn);
@@ -114,7 +130,8 @@ int check_dual(const char* fn, const void* input, int64_t rows, int64_t cols, co
   REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", fn);
   REQUIRE(rows % 32 == 0 && cols % 32 == 0, "%s: rows and cols must be multiples of 32 (got %lld x %lld)", fn,
           (long long)rows, (long long)cols);
-  REQUIRE((rows / 32 + 1) * (cols / 256 + 1) < ((int64_t)1 << 30), "%s: too many tiles", fn);
+  const int64_t tiles = size_mul(rows / 32 + 1, cols / 256 + 1);
+  REQUIRE(tiles >= 0 && tiles < ((int64_t)1 << 30), "%s: too many tiles", fn);
   const int64_t n = rows * cols;
   REQUIRE_BUF("input", input, n, n);
   REQUIRE_BUF("row_q", row_q, row_q_bytes, n / 2);
@@ -173,6 +190,7 @@ int omo_hip_per_token_Mxfp4ToBf16_dequant(const void* input, int64_t input_bytes
   (void)output_s; (void)output_s_bytes; (void)group_size; (void)eps; (void)fp4_min; (void)fp4_max;
   if (scale_ue8m0) return fail(OMO_ERR_UNSUPPORTED, "%s: scale_ue8m0 is not supported (the reference asserts it off)", fn);
   REQUIRE(input_bytes >= 0 && input_bytes % 128 == 0, "%s: input.numel() %% 128 != 0", fn);
+  REQUIRE(input_bytes <= kMaxSize, "%s: shape too large", fn);
   REQUIRE_BUF("input", input, input_bytes, input_bytes);
   REQUIRE_BUF("input_s", input_s, input_s_bytes, input_bytes / 16);
   REQUIRE_BUF("output_q", output_q, output_q_elems, 2 * input_bytes);
@@ -230,6 +248,7 @@ int omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(const void* input, int64_t rows, in
                                              int64_t output_s_rows, int64_t output_s_cols, float eps, void* stream) {
   const char* fn = "omo_per_token_Mxfp4RowToBf16ToFp8Col";
   REQUIRE(rows >= 0 && row_bytes >= 0, "%s: negative shape", fn);
+  REQUIRE(row_bytes <= kMaxSize / 2 && size_mul(rows, 2 * row_bytes) >= 0, "%s: shape too large", fn);
   const int64_t M = rows, N = row_bytes * 2;
   // the shape checks of per_token_Mxfp4RowToBf16ToFp8Col.cu:219-224
   REQUIRE(input_s_rows == M, "%s: input_s.size(0) != M", fn);
@@ -258,7 +277,11 @@ int omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(const void* input, int64_t r
   REQUIRE(rows >= 0 && row_bytes >= 0 && num_splits >= 0 && max_split_len >= 0, "%s: negative shape", fn);
   REQUIRE(num_splits <= 65535, "%s: at most 65535 splits", fn);
   REQUIRE(!std::isnan(eps), "%s: eps is NaN", fn);
+  REQUIRE(row_bytes <= kMaxSize / 2 && size_mul(rows, 2 * row_bytes) >= 0, "%s: shape too large", fn);
   const int64_t M = rows, N = row_bytes * 2;
+  // Every split the kernel converts lies inside the M rows, so a longer
+  // max_split_len only adds workgroups that exit at once.
+  if (max_split_len > M) max_split_len = M;
   REQUIRE_BUF("input", input, M * row_bytes, M * row_bytes);
   // the kernel reads scale byte row*(N/32) + col/32 for rows < M, cols < N
   const int64_t s_need = M == 0 || N == 0 ? 0 : (M - 1) * (N / 32) + (N - 1) / 32 + 1;

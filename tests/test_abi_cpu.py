@@ -225,3 +225,34 @@ def test_dual_grouped_validation_paths():
     assert lib.omo_hip_quant_mxfp4_dual_grouped(arr, 1, float("nan"), None) == -1
     assert lib.omo_hip_quant_mxfp4_dual_grouped(None, 3, 1e-10, None) == -1
     assert lib.omo_hip_quant_mxfp4_dual_grouped(None, 0, 1e-10, None) == 0
+
+
+def test_oversized_shapes_rejected():
+    """Shapes whose byte counts overflow 64-bit arithmetic are refused before
+    any size check could wrap (fake pointers, never dereferenced)."""
+    lib = _lib()
+    f = ctypes.c_void_p(0x1000)
+    big = 1 << 62
+
+    def refused(rc, what=b"too large"):
+        assert rc == -1 and what in lib.omo_hip_last_error(), lib.omo_hip_last_error()
+
+    refused(lib.omo_hip_per_token_Mxfp4ToBf16_dequant(f, big, f, big, f, big, None, 0, 32, 1e-10, -6.0, 6.0, 0, None))
+    for fn in (lib.omo_hip_per_token_Mxfp4ToFp8, lib.omo_hip_per_token_Mxfp4ToBf16ToFp8,
+               lib.omo_hip_per_token_Mxfp4ToFp8_col):
+        refused(fn(f, 1 << 40, 1 << 30, f, big, f, big, f, big, 128, 1e-10, -6.0, 6.0, 0, None))
+    # 2^34 x 2^31 bytes wraps to 0 in int64, a multiple of everything
+    refused(lib.omo_hip_per_token_Mxfp4ToFp8(f, 1 << 33, 1 << 31, f, big, f, big, f, big, 128, 1e-10, -6.0, 6.0, 0,
+                                             None))
+    refused(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(f, 1 << 40, 1 << 30, f, 1 << 40, 1 << 26, f, 1 << 31,
+                                                         1 << 40, f, 1 << 33, 1 << 31, 1e-10, None))
+    refused(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(f, 1, big, f, 1, 1, f, 1, 1, f, 1, 1, 1e-10, None))
+    refused(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(f, 1 << 40, 1 << 30, f, big, f, big, f, big, f, f, f,
+                                                                1, 1 << 40, 1e-10, None))
+    refused(lib.omo_hip_quant_mxfp4_dual(f, 1 << 40, 1 << 40, f, big, f, big, f, big, f, big, 1e-10, None),
+            b"too many tiles")
+    refused(lib.omo_hip_mxfp4_permute_rows(f, big, 1 << 61, f, big, 4, 4, 128, f, 4, f, 256, f, 16, None))
+    refused(lib.omo_hip_mxfp4_permute_rows(f, big, 1 << 40, f, big, 1 << 40, 1 << 30, 128, f, 4, f, 256, f, 16,
+                                           None))
+    refused(lib.omo_hip_permute_Mxfp4ToFp8(f, 1 << 20, 1 << 40, f, 1 << 20, 1 << 36, 1, 1 << 40, f, 1 << 30, f, big,
+                                           f, big, None))
