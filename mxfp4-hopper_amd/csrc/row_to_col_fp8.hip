@@ -36,6 +36,8 @@
 // or NaN, and v_cvt_scalef32_pk_f32_fp4 gives both columns' exact fp32
 // values of a row in one instruction; otherwise the lane restates the
 // reference per element.
+#include <algorithm>
+
 #include "omo_device.cuh"
 #include "omo_internal.h"
 
@@ -453,6 +455,7 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_kernel(const uint8_
 // whole aligned tensors (every workgroup resident at once on the benchmark
 // shapes: 896 tiles at 4096 x 7168) and by the per-split kernel.
 constexpr int kWideCols = 256;
+constexpr int64_t kMaxGridYZ = 65535;  // below the y and z grid limits (65536)
 constexpr int kWidePitch = 128 + 32;  // 16 B aligned LDS rows; 40 dwords keep a wave's row reads on distinct banks
 
 struct WideSmem {
@@ -749,9 +752,9 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8
 __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_wide_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
-    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool out_line) {
+    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool out_line, int64_t bm0, int64_t bn0) {
   __shared__ WideSmem sm;
-  const int64_t split = blockIdx.x, bm = blockIdx.y, bn = blockIdx.z;
+  const int64_t split = blockIdx.x, bm = bm0 + blockIdx.y, bn = bn0 + blockIdx.z;
   const int64_t len = lens[split];
   if (bm * kTile >= len) return;
   const int64_t start = offs[split], sstart = soffs[split];
@@ -773,9 +776,9 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_wide_kernel(
 __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
-    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs) {
+    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs, int64_t bm0, int64_t bn0) {
   __shared__ RowColSmem sm;
-  const int64_t split = blockIdx.x, bm = blockIdx.y, bn = blockIdx.z;
+  const int64_t split = blockIdx.x, bm = bm0 + blockIdx.y, bn = bn0 + blockIdx.z;
   const int64_t len = lens[split];
   if (bm * kTile >= len) return;
   const int64_t start = offs[split], sstart = soffs[split];
@@ -829,22 +832,33 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   if (nsplits == 0 || max_split_len <= 0 || N == 0) return hipSuccess;
   const bool vin = (N % 32 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
   const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
-  if (vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
-    dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)(N / kWideCols));
-    // Unused dynamic LDS caps residency at 4 workgroups per CU (6 by the
-    // kernel's own LDS and registers): fewer tiles' partial output lines wait
-    // in L2 at once. Ragged cfg5 splits: 49.6 us against 51.0, and 59.8 against
-    // 62.8 right after a 512 MB fill (dirty caches, as in a layer step).
-    const int per_wg = current_device_caps().lds_per_workgroup / 4 - 2560;
-    const size_t reserve = per_wg > (int)sizeof(WideSmem) ? (size_t)(per_wg - (int)sizeof(WideSmem)) : 0;
-    return launch(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
-                       static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs,
-                       total_rows, N, out_s_rows, eps, (reinterpret_cast<uintptr_t>(out) & 127) == 0);
+  const bool wide = vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0;
+  const int64_t tiles_m = (max_split_len + kTile - 1) / kTile;
+  const int64_t bands = wide ? N / kWideCols : (N + kTile - 1) / kTile;
+  // Unused dynamic LDS caps the wide kernel's residency at 4 workgroups per
+  // CU (6 by its own LDS and registers): fewer tiles' partial output lines
+  // wait in L2 at once. Ragged cfg5 splits: 49.6 us against 51.0, and 59.8
+  // against 62.8 right after a 512 MB fill (dirty caches, as in a layer step).
+  const int per_wg = current_device_caps().lds_per_workgroup / 4 - 2560;
+  const size_t reserve = per_wg > (int)sizeof(WideSmem) ? (size_t)(per_wg - (int)sizeof(WideSmem)) : 0;
+  const bool out_line = (reinterpret_cast<uintptr_t>(out) & 127) == 0;
+  // Grid y (row tiles) and z (column bands) hold at most 65536 each: longer
+  // splits or wider rows take several launches over offset ranges.
+  for (int64_t bm0 = 0; bm0 < tiles_m; bm0 += kMaxGridYZ) {
+    for (int64_t bn0 = 0; bn0 < bands; bn0 += kMaxGridYZ) {
+      const dim3 grid((unsigned)nsplits, (unsigned)std::min<int64_t>(tiles_m - bm0, kMaxGridYZ),
+                      (unsigned)std::min<int64_t>(bands - bn0, kMaxGridYZ));
+      const hipError_t e =
+          wide ? launch(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), reserve, stream,
+                        static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out),
+                        out_s, lens, offs, soffs, total_rows, N, out_s_rows, eps, out_line, bm0, bn0)
+               : launch(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream,
+                        static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out),
+                        out_s, lens, offs, soffs, total_rows, N, out_s_rows, eps, vin, vs, bm0, bn0);
+      if (e != hipSuccess) return e;
+    }
   }
-  dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + kTile - 1) / kTile), (unsigned)((N + kTile - 1) / kTile));
-  return launch(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
-                     static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
-                     out_s_rows, eps, vin, vs);
+  return hipSuccess;
 }
 
 }  // namespace omo_hip

@@ -136,3 +136,57 @@ def test_dual_past_2_31(oracle, dev):
         eq, es = oracle.quant_mxfp4(xt.reshape(-1))
         np.testing.assert_array_equal(bits_u8(cq[c0:c0 + 256]).reshape(-1), eq)
         np.testing.assert_array_equal(bits_u8(cs[c0:c0 + 256]).reshape(-1), es)
+
+
+def _msplit_gpu(dev, q, s, splits):
+    import omo
+    from omo_python_api.mxfp4_dequant import split_metadata
+    R, N = q.size(0), q.size(1) * 2
+    lens, offs, soffs, mx, _, srows = split_metadata(splits, dev)
+    out = torch.empty(R * N, dtype=torch.float8_e4m3fn, device=dev)
+    outs = torch.empty((srows, N), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(q, s, out, outs, lens, offs, soffs, mx, 1e-10)
+    torch.cuda.synchronize()
+    return out, outs
+
+
+def test_msplit_more_row_tiles_than_grid_y(oracle, dev):
+    """A split of 8,400,037 rows has 65,626 row tiles, past the 65,536 that
+    grid y holds, so the launch is split over row-tile ranges: row windows at
+    the start, across tile 65,535 and at the end against the oracle."""
+    splits, N = [8_400_037, 300], 256
+    R = sum(splits)
+    _say("msplit long split", splits, N)
+    q, s = _gpu_codes(dev, R, N, 34)
+    out, outs = _msplit_gpu(dev, q, s, splits)
+    ys = out[:splits[0] * N].view(N, splits[0])
+    for r0, w in ((0, 256), (65535 * 128 - 256, 512), (65624 * 128, splits[0] - 65624 * 128)):
+        eo, es = oracle.row_to_fp8_col_msplit(bits_u8(q[r0:r0 + w]), bits_u8(s[r0:r0 + w]), [w])
+        np.testing.assert_array_equal(bits_u8(ys[:, r0:r0 + w]).reshape(-1), eo)
+        t0 = r0 // 128
+        np.testing.assert_array_equal(outs[t0:t0 + es.shape[0]].cpu().numpy().view(np.uint32), es.view(np.uint32))
+    eo, es = oracle.row_to_fp8_col_msplit(bits_u8(q[splits[0]:]), bits_u8(s[splits[0]:]), splits[1:])
+    np.testing.assert_array_equal(bits_u8(out[splits[0] * N:]), eo)
+    np.testing.assert_array_equal(outs[-es.shape[0]:].cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+@pytest.mark.parametrize("N", [65536 * 256 + 256, 65536 * 128 + 128])
+def test_msplit_more_column_bands_than_grid_z(oracle, dev, N):
+    """Rows of 16.8M (256-column bands, the wide kernel) or 8.4M columns
+    (128-column bands, the general kernel) have more than the 65,536 column
+    bands grid z holds: column windows at the start and across the last band
+    boundaries against the oracle on those columns."""
+    splits = [128, 1, 77]
+    R = sum(splits)
+    _say("msplit wide rows", splits, N)
+    q, s = _gpu_codes(dev, R, N, 35)
+    out, outs = _msplit_gpu(dev, q, s, splits)
+    for c0, w in ((0, 256), (N - 768, 768)):
+        eo, es = oracle.row_to_fp8_col_msplit(bits_u8(q[:, c0 // 2:(c0 + w) // 2]), bits_u8(s[:, c0 // 32:(c0 + w) // 32]),
+                                              splits)
+        got, o = [], 0
+        for m in splits:
+            got.append(bits_u8(out[o * N:(o + m) * N].view(N, m)[c0:c0 + w]).reshape(-1))
+            o += m
+        np.testing.assert_array_equal(np.concatenate(got), eo)
+        np.testing.assert_array_equal(outs[:, c0:c0 + w].cpu().numpy().view(np.uint32), es.view(np.uint32))
