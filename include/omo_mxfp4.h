@@ -13,7 +13,8 @@
  * Every function validates its arguments before touching the GPU and
  * returns OMO_OK or a negative status; omo_hip_last_error() then describes
  * the failure (thread-local). Sizes are element counts unless named
- * *_bytes. Data layouts (bit patterns) are those of the reference:
+ * *_bytes; products of sizes are formed without wrapping, and a shape whose
+ * byte count passes 2^60 is refused. Data layouts (bit patterns) are those of the reference:
  *   bf16      : 16-bit patterns, row-major
  *   codes     : uint8, two E2M1 nibbles per byte, element 2j in the low nibble
  *   scales    : uint8 E8M0, byte s means 2^(s-127), one per 32 elements
