@@ -20,9 +20,23 @@ Rules restated (reference lines):
     g = (uint16)(max of the 4 scale bytes - 6), pattern = bits(code) -
     ((uint16)(g - s_i) << 7) mod 2^16, clamp to +-448, E4M3 nearest-even;
     scale = fp32 bits (uint8)g << 23.
+  * row -> col FP8, dense (per_token_Mxfp4RowToBf16ToFp8Col.cu:80-190): v =
+    e2m1(code) * 2^(s-127) in fp32 (s = 0 -> 0, s = 255 -> inf); per column of
+    a 128-row tile amax = fmaxf over |v| seeded with eps (rows past M count as
+    0); scale row = amax / 448; q = clamp(v * m, -448, 448) with m = 448 / amax
+    when amax > 1e-9f, else 0 (NaN -> -448), E4M3 nearest-even.
+  * row -> col FP8, per split (per_token_Mxfp4RowToBf16ToFp8Col_msplit.cu:19-41,
+    150-221): tiles restart at each split; amax seeded with 0; m = 1.0 when
+    amax <= eps, else 1 / 2^e with 2^e the fp32 exponent of amax / 448 rounded
+    up (0 -> m = inf); scale row = 1 / m; output column c of split i at
+    offset_i * N + c * len_i.
+  Every fp32 operation is restated as the exact rational result rounded to
+  fp32 (nearest-even, subnormals kept), with IEEE zero signs, infinities and
+  NaN handled explicitly.
 
 Run: python tests/golden/make_golden.py   (writes the *.json files here)
 """
+import base64
 import json
 import math
 import os
@@ -215,6 +229,219 @@ def requant_group(codes64, s4):
     return bytes(out), (g16 & 0xFF) << 23
 
 
+# ---------------------------------------------------------------- fp32 model
+def rne32(mag):
+    """Exact positive Fraction -> nearest float32 value (nearest-even,
+    subnormals kept) as a Python float, or inf past the largest finite."""
+    e = mag.numerator.bit_length() - mag.denominator.bit_length()
+    while Fraction(2) ** e > mag:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= mag:
+        e += 1
+    ulp = Fraction(2) ** (max(e, -126) - 23)
+    n = mag / ulp
+    k = math.floor(n)
+    r = n - k
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and k % 2 == 1):
+        k += 1
+    val = k * ulp
+    if val >= Fraction(2) ** 128:
+        return float("inf")
+    return float(val)  # a float32 value is exact in a double
+
+
+def _neg(x):
+    return math.copysign(1.0, x) < 0
+
+
+def mul32(a, b):
+    """IEEE float32 product of two float32 values (Python floats)."""
+    if math.isnan(a) or math.isnan(b):
+        return float("nan")
+    sign = _neg(a) != _neg(b)
+    if math.isinf(a) or math.isinf(b):
+        if a == 0 or b == 0:
+            return float("nan")
+        return -math.inf if sign else math.inf
+    prod = Fraction(a) * Fraction(b)
+    if prod == 0:
+        return -0.0 if sign else 0.0
+    r = rne32(abs(prod))
+    return -r if sign else r
+
+
+def div32(a, b):
+    """IEEE float32 quotient of two float32 values."""
+    if math.isnan(a) or math.isnan(b) or (a == 0 and b == 0) or (math.isinf(a) and math.isinf(b)):
+        return float("nan")
+    sign = _neg(a) != _neg(b)
+    if math.isinf(a) or b == 0:
+        return -math.inf if sign else math.inf
+    if math.isinf(b) or a == 0:
+        return -0.0 if sign else 0.0
+    r = rne32(abs(Fraction(a) / Fraction(b)))
+    return -r if sign else r
+
+
+def fmaxf(a, b):
+    if math.isnan(a):
+        return b
+    if math.isnan(b):
+        return a
+    return a if a >= b else b
+
+
+def fminf(a, b):
+    if math.isnan(a):
+        return b
+    if math.isnan(b):
+        return a
+    return a if a <= b else b
+
+
+def f32_bits(x):
+    return int(np.array([x], np.float32).view(np.uint32)[0])
+
+
+def f32_from_bits(b):
+    return float(np.array([b & 0xFFFFFFFF], np.uint32).view(np.float32)[0])
+
+
+def fp8_of(q):
+    """E4M3 byte of a clamped float32 value (|q| <= 448), zero signs kept."""
+    if q == 0:
+        return 0x80 if _neg(q) else 0x00
+    return e4m3_rne(Fraction(q))
+
+
+def decode32(nib, s):
+    """fp32 value of a code under a scale byte: bf16(e2m1) * bf16(s << 7)."""
+    v = float(e2m1_bf16_value(nib))
+    if nib & 8 and v == 0:
+        v = -0.0
+    d = 0.0 if s == 0 else (math.inf if s == 255 else float(Fraction(2) ** (s - 127)))
+    return mul32(v, d)
+
+
+def _decode_rows(codes, scales, N):
+    """codes [M, N/2] bytes, scales [M, N/32] bytes -> rows of fp32 values."""
+    rows = []
+    for r in range(len(codes)):
+        rows.append([decode32((codes[r][c // 2] >> (4 * (c & 1))) & 0xF, scales[r][c // 32]) for c in range(N)])
+    return rows
+
+
+def row_to_col_dense(codes, scales, N, eps):
+    """Dense row -> col FP8: (fp8 [N][M] bytes, fp32 bits [ceil(M/128)][N])."""
+    M = len(codes)
+    v = _decode_rows(codes, scales, N)
+    eps32 = float(np.float32(eps))
+    thr = float(np.float32(1e-9))
+    out = [[0] * M for _ in range(N)]
+    srows = []
+    for t0 in range(0, M, 128):
+        rows = range(t0, min(t0 + 128, M))
+        srow = []
+        for c in range(N):
+            amax = eps32
+            for r in rows:
+                amax = fmaxf(amax, abs(v[r][c]))
+            srow.append(f32_bits(div32(amax, 448.0)))
+            m = div32(448.0, amax) if amax > thr else 0.0
+            for r in rows:
+                q = fminf(fmaxf(mul32(v[r][c], m), -448.0), 448.0)
+                out[c][r] = fp8_of(q)
+        srows.append(srow)
+    return out, srows
+
+
+def te_pow2_multiplier(amax, eps):
+    """The per-split multiplier: 1.0 when amax <= eps, else 1 / 2^e with 2^e
+    the fp32 exponent of amax / 448 rounded up (divisor 0 -> inf)."""
+    if amax <= eps:
+        return 1.0
+    bits = f32_bits(div32(amax, 448.0))
+    e = (bits >> 23) & 0xFF
+    if bits & 0x7FFFFF:
+        e += 1
+    divisor = f32_from_bits(e << 23)
+    if divisor == 0:
+        return math.inf
+    if math.isinf(divisor):
+        return 0.0
+    return float(np.float32(Fraction(1) / Fraction(divisor)))  # a power of two, exact
+
+
+def row_to_col_msplit(codes, scales, N, splits, eps):
+    """Per-split row -> col FP8: (flat fp8 bytes, fp32 bits [sum ceil(len/128)][N])."""
+    v = _decode_rows(codes, scales, N)
+    eps32 = float(np.float32(eps))
+    out = [0] * (len(codes) * N)
+    srows = []
+    off = 0
+    for ln in splits:
+        for t0 in range(0, ln, 128):
+            rows = range(off + t0, off + min(t0 + 128, ln))
+            srow = []
+            for c in range(N):
+                amax = 0.0
+                for r in rows:
+                    amax = fmaxf(amax, abs(v[r][c]))
+                m = te_pow2_multiplier(amax, eps32)
+                srow.append(f32_bits(div32(1.0, m)))
+                for r in rows:
+                    q = fminf(fmaxf(mul32(v[r][c], m), -448.0), 448.0)
+                    out[off * N + c * ln + (r - off)] = fp8_of(q)
+            srows.append(srow)
+        off += ln
+    return out, srows
+
+
+def _tile_inputs(rng, M, N, base, spread, specials):
+    codes = [bytes(rng.integers(0, 256, N // 2, dtype=np.uint8)) for _ in range(M)]
+    scales = [[max(0, min(255, base + int(rng.integers(-spread, spread + 1)))) for _ in range(N // 32)]
+              for _ in range(M)]
+    if specials:
+        for r in range(M):
+            scales[r][0] = 255 if r % 37 == 5 else scales[r][0]    # inf / NaN elements in block 0
+            if N // 32 > 1:
+                scales[r][1] = 0                                    # block 1: zeros
+            if N // 32 > 2 and r % 3 == 0:
+                scales[r][2] = int(rng.integers(1, 4))              # subnormal products
+            if N // 32 > 4:
+                scales[r][3] = 93                                   # column maxima at most 6 * 2^-34 (< 1e-9)
+                scales[r][4] = 2                                    # every product subnormal
+        codes[3] = bytes(N // 2)                                    # a zero row
+    return codes, scales
+
+
+def _b64(b):
+    return base64.b64encode(b).decode()
+
+
+def row_to_col_cases():
+    rng = np.random.default_rng(20261202)
+    dense, msplit = [], []
+    for M, N, eps, base, spread, specials in ((130, 64, 1e-10, 127, 6, False), (130, 256, 1e-10, 120, 20, True),
+                                              (40, 128, 3.0, 127, 2, True), (1, 64, 1e-10, 127, 0, False)):
+        codes, scales = _tile_inputs(rng, M, N, base, spread, specials)
+        out, srows = row_to_col_dense(codes, scales, N, eps)
+        dense.append({"M": M, "N": N, "eps": eps, "codes": _b64(b"".join(codes)),
+                      "scales": _b64(bytes(b for row in scales for b in row)),
+                      "fp8": _b64(bytes(b for col in out for b in col)), "scale_bits": srows})
+    for splits, N, eps, base, spread, specials in (([1, 127, 130], 64, 1e-10, 127, 6, False),
+                                                   ([0, 5, 129], 256, 1e-10, 118, 25, True),
+                                                   ([40, 3], 64, -1.0, 127, 3, True),
+                                                   ([40], 256, 1e5, 140, 2, False)):
+        M = sum(splits)
+        codes, scales = _tile_inputs(rng, M, N, base, spread, specials)
+        out, srows = row_to_col_msplit(codes, scales, N, splits, eps)
+        msplit.append({"splits": splits, "N": N, "eps": eps, "codes": _b64(b"".join(codes)),
+                       "scales": _b64(bytes(b for row in scales for b in row)), "fp8": _b64(bytes(out)),
+                       "scale_bits": srows})
+    return dense, msplit
+
+
 def bf16_bits_of(x):
     return int(np.array([x], np.float32).view(np.uint32)[0] >> 16)
 
@@ -277,7 +504,13 @@ def main():
         json.dump({"note": "bf16 bits of code (0..15) under scale byte; null = unpinned NaN", "table": deq}, f)
     with open(os.path.join(HERE, "fp8_rowwise_groups.json"), "w") as f:
         json.dump({"groups": groups}, f, indent=0)
-    print(f"{len(quant)} quantize blocks, 256x16 dequant entries, {len(groups)} FP8 groups")
+    dense, msplit = row_to_col_cases()
+    with open(os.path.join(HERE, "row_to_col_fp8.json"), "w") as f:
+        json.dump({"note": "codes, scales and fp8 are base64; fp8 is [N][M] (dense) or the flat per-split "
+                           "layout; scale_bits are fp32 bit patterns [tile row][N]", "dense": dense,
+                   "msplit": msplit}, f)
+    print(f"{len(quant)} quantize blocks, 256x16 dequant entries, {len(groups)} FP8 groups, "
+          f"{len(dense)} dense and {len(msplit)} per-split row->col cases")
 
 
 if __name__ == "__main__":

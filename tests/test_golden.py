@@ -6,6 +6,7 @@ oracle/mxfp4_oracle.c (the reference itself ships no golden vectors). The
 CPU tests pin the oracle to them; the GPU tests run the same vectors through
 the C ABI.
 """
+import base64
 import json
 import os
 
@@ -51,6 +52,20 @@ def fp8_vectors():
     return codes, scales, fp8, sbits
 
 
+def row_to_col_vectors(kind):
+    """Dense or per-split row -> col FP8 cases: dicts with codes [M, N/2],
+    scales [M, N/32], expected fp8 bytes and scale-row bit patterns."""
+    cases = []
+    for c in _load("row_to_col_fp8.json")[kind]:
+        N = c["N"]
+        M = c["M"] if kind == "dense" else sum(c["splits"])
+        b = {k: np.frombuffer(base64.b64decode(c[k]), np.uint8) for k in ("codes", "scales", "fp8")}
+        cases.append({"M": M, "N": N, "eps": c["eps"], "splits": c.get("splits"),
+                      "codes": b["codes"].reshape(M, N // 2), "scales": b["scales"].reshape(M, N // 32),
+                      "fp8": b["fp8"], "scale_bits": np.array(c["scale_bits"], np.uint32).reshape(-1, N)})
+    return cases
+
+
 def _check_dequant(out_bits, table):
     checked = 0
     for s in range(256):
@@ -82,6 +97,20 @@ def test_golden_fp8_rowwise_oracle(oracle):
     o, os_ = oracle.mxfp4_to_fp8(codes, scales)
     np.testing.assert_array_equal(o, fp8)
     np.testing.assert_array_equal(os_.view(np.uint32)[0], sbits)
+
+
+def test_golden_row_to_col_oracle(oracle):
+    for c in row_to_col_vectors("dense"):
+        o, os_ = oracle.row_to_fp8_col(c["codes"], c["scales"], eps=c["eps"])
+        np.testing.assert_array_equal(o.reshape(-1), c["fp8"], err_msg=f"{c['M']}x{c['N']} eps {c['eps']}")
+        np.testing.assert_array_equal(os_.view(np.uint32), c["scale_bits"])
+
+
+def test_golden_msplit_oracle(oracle):
+    for c in row_to_col_vectors("msplit"):
+        o, os_ = oracle.row_to_fp8_col_msplit(c["codes"], c["scales"], c["splits"], eps=c["eps"])
+        np.testing.assert_array_equal(o, c["fp8"], err_msg=f"{c['splits']} {c['N']} eps {c['eps']}")
+        np.testing.assert_array_equal(os_.view(np.uint32), c["scale_bits"])
 
 
 # ------------------------------------------------------------------ GPU: HIP path
@@ -121,3 +150,30 @@ def test_golden_fp8_rowwise_gpu(dev):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bits_u8(out), fp8)
     np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32)[0], sbits)
+
+
+@pytest.mark.gpu
+def test_golden_row_to_col_gpu(dev):
+    import omo
+    for c in row_to_col_vectors("dense"):
+        M, N = c["M"], c["N"]
+        out = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=dev)
+        outs = torch.empty(((M + 127) // 128, N), dtype=torch.float32, device=dev)
+        omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(c["codes"].copy()).to(dev),
+                                                torch.from_numpy(c["scales"].copy()).to(dev), out, outs, c["eps"])
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits_u8(out).reshape(-1), c["fp8"], err_msg=f"{M}x{N} eps {c['eps']}")
+        np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), c["scale_bits"])
+
+
+@pytest.mark.gpu
+def test_golden_msplit_gpu(dev):
+    from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper
+    for c in row_to_col_vectors("msplit"):
+        ys, ss = omo_per_token_mxfp4RowToBf16ToFp8Col_msplit_wrapper(
+            torch.from_numpy(c["codes"].copy()).to(dev), torch.from_numpy(c["scales"].copy()).to(dev), c["splits"],
+            eps=c["eps"])
+        torch.cuda.synchronize()
+        got = np.concatenate([bits_u8(y).reshape(-1) for y in ys])
+        np.testing.assert_array_equal(got, c["fp8"], err_msg=f"{c['splits']} {c['N']} eps {c['eps']}")
+        np.testing.assert_array_equal(torch.cat(ss).cpu().numpy().view(np.uint32), c["scale_bits"])
