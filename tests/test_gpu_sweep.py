@@ -16,7 +16,7 @@ from helpers import bits_u16, bits_u8, from_u16
 pytestmark = pytest.mark.gpu
 
 FP8 = torch.float8_e4m3fn
-N_CASES = 480
+N_CASES = 484
 SPECIALS = np.array([0x7FC0, 0xFFC0, 0x7F81, 0x7F80, 0xFF80, 0x0000, 0x8000, 0x0001, 0x807F, 0x7F7F, 0xFF7F, 0x0080],
                     np.uint16)
 EPS = [1e-10, 0.0, -1.0, 1e-3, 3.0, 1e5]
@@ -217,15 +217,63 @@ class Sweep:
         _eq(_scales_bits(f8s), es.view(np.uint32), "gathered FP8 scales")
         return f"permute {T}x{H} -> {n} rows"
 
+    def dequant_raw(self):
+        r = self.rng
+        n = 128 * int(r.integers(1, 4000))
+        q = r.integers(0, 256, n, dtype=np.uint8)
+        if r.random() < 0.5:
+            s = r.integers(0, 256, n // 16, dtype=np.uint8)
+        else:
+            s = np.clip(127 + r.integers(-30, 30, n // 16), 0, 255).astype(np.uint8)
+        out = torch.empty(2 * n, dtype=torch.bfloat16, device=self.dev)
+        self.omo.omo_per_token_Mxfp4ToBf16_dequant(self.t(q), self.t(s), out, torch.empty((1, 1), device=self.dev), 32,
+                                                   1e-10, -6.0, 6.0, False)
+        torch.cuda.synchronize()
+        _eq(bits_u16(out), self.o.dequant_bf16(q, s), "dequant of random bytes")
+        return f"dequant {n} code bytes"
+
+    def dual_grouped(self):
+        r = self.rng
+        shapes = []
+        for _ in range(int(r.integers(1, 7))):
+            if r.random() < 0.5:
+                shapes.append((32 * int(r.integers(0, 20)), 32 * int(r.integers(1, 20))))
+            else:
+                shapes.append((64 * int(r.integers(1, 10)), 256 * int(r.integers(1, 4))))
+        xs = [self.bf16_values(M * K).reshape(M, K) for M, K in shapes]
+        outs = [[torch.empty(sh, dtype=torch.uint8, device=self.dev)
+                 for sh in ((M, K // 2), (M, K // 32), (K, M // 2), (K, M // 32))] for M, K in shapes]
+        self.omo.omo_quant_mxfp4_dual_grouped([from_u16(x, self.dev) for x in xs], outs)
+        torch.cuda.synchronize()
+        for x, o in zip(xs, outs):
+            rq, rs = self.o.quant_mxfp4(x.reshape(-1))
+            cq, cs = self.o.quant_mxfp4(np.ascontiguousarray(x.T).reshape(-1))
+            for got, want, name in zip(o, (rq, rs, cq, cs), ("row codes", "row scales", "column codes",
+                                                             "column scales")):
+                _eq(bits_u8(got).reshape(-1), want, "grouped dual layout " + name)
+        return f"grouped dual layout {shapes}"
+
+    def payload_dequant(self):
+        r = self.rng
+        T, H = int(r.integers(1, 400)), 256 * int(r.integers(1, 30))
+        q, s = self.codes_scales(T, H // 2)
+        pay = self.t(np.concatenate([q, s], 1))
+        y = torch.empty((T, H), dtype=torch.bfloat16, device=self.dev)
+        self.omo.omo_packed_Mxfp4ToBf16_dequant(pay, y)
+        torch.cuda.synchronize()
+        _eq(bits_u16(y).reshape(-1), self.o.dequant_bf16(q.reshape(-1), s.reshape(-1)), "payload dequant")
+        return f"payload dequant {T}x{H}"
+
 
 def test_randomized_sweep(oracle, dev):
     sw = Sweep(oracle, dev, seed=20261202)
-    cases = [sw.quant, sw.fp8_rows, sw.fp8_col, sw.row_to_col, sw.msplit, sw.dual, sw.packed, sw.permute]
+    cases = [sw.quant, sw.dequant_raw, sw.fp8_rows, sw.fp8_col, sw.row_to_col, sw.msplit, sw.dual, sw.dual_grouped,
+             sw.packed, sw.payload_dequant, sw.permute]
     for i in range(N_CASES):
         case = cases[i % len(cases)]
         try:
             desc = case()
         except AssertionError as e:
             raise AssertionError(f"sweep case {i} ({case.__name__}, seed 20261202): {e}") from None
-        if i % 60 == 0:
+        if i % 44 == 0:
             print("[case]", i, desc, flush=True)
