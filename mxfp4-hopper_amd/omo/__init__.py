@@ -77,6 +77,12 @@ def _nbytes(t: torch.Tensor) -> int:
     return t.numel() * t.element_size()
 
 
+# torch's raw current-stream getter (a few tens of ns) where this torch build
+# has it; the public torch.cuda.current_stream(...).cuda_stream builds a Stream
+# object per call (about 2 us, a quarter of this binding's host time).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 class _on_device:
     """Make ``t``'s device current for the launch (the library launches on
     the current HIP device) and yield its current stream handle."""
@@ -85,13 +91,17 @@ class _on_device:
         self.dev = t.device
 
     def __enter__(self):
+        idx = self.dev.index if self.dev.index is not None else torch.cuda.current_device()
         self.prev = torch.cuda.current_device()
-        if self.dev.index is not None and self.dev.index != self.prev:
-            torch.cuda.set_device(self.dev)
-        return torch.cuda.current_stream(self.dev).cuda_stream
+        self.switched = idx != self.prev
+        if self.switched:
+            torch.cuda.set_device(idx)
+        if _raw_stream is not None:
+            return _raw_stream(idx)
+        return torch.cuda.current_stream(idx).cuda_stream
 
     def __exit__(self, *exc):
-        if torch.cuda.current_device() != self.prev:
+        if self.switched:
             torch.cuda.set_device(self.prev)
         return False
 
