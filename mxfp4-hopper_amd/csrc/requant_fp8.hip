@@ -83,9 +83,13 @@ __device__ __forceinline__ u32x2 to_fp8_dword_ref(uint32_t c, uint32_t offset) {
 // of it is assembled from partial writes of several workgroups on different
 // XCDs. FP8 bytes are written non-temporally; codes are read with ordinary
 // loads (non-temporal code loads made this kernel and the transposed one
-// 15-16% slower).
+// 15-16% slower). Inputs of few rows take 8-row tiles instead (ROWS), so that
+// a launch still spreads over the CUs: 128 x 7168 ran 3.2 us in 56 tiles of
+// 32 rows; its scale runs are then 32 B pieces of lines that four
+// workgroups share.
 constexpr int kRqGroups = 4;
 constexpr int kRqRows = 32;
+constexpr int kRqRowsSmall = 8;
 // Codes of row r start at q + r * q_stride and its scale bytes at
 // s + r * s_stride (bytes): contiguous [M, Kb] + [M, Kb/16] tensors, or the
 // expert-parallel payload rows [codes | scales] read in place. ALIGN8: the
@@ -94,13 +98,14 @@ constexpr int kRqRows = 32;
 // expert-major token order of a MoE permutation); an index outside
 // [0, n_src) reads zero codes and zero scale bytes, i.e. the row a permutation
 // pads with zeros, requantized.
-template <int UNROLL, bool ALIGN8>
+template <int ROWS, bool ALIGN8>
 __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __restrict__ q, int64_t q_stride,
                                                            const uint8_t* __restrict__ s, int64_t s_stride,
                                                            const int32_t* __restrict__ src, int64_t n_src,
                                                            u32x4* __restrict__ out, float* __restrict__ out_s,
                                                            uint32_t M, uint32_t gpr, uint32_t gx) {
   constexpr int PPR = 8 * kRqGroups;  // pairs per tile row
+  constexpr int UNROLL = ROWS * PPR / 256;
   const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x);
   const uint32_t bx = L % gx, by = L / gx;
   const int64_t ppr_all = 8 * (int64_t)gpr;
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int e = u * 256 + threadIdx.x;
-    const uint32_t r = by * kRqRows + e / PPR, cp = bx * PPR + e % PPR;
+    const uint32_t r = by * ROWS + e / PPR, cp = bx * PPR + e % PPR;
     if (r < M && cp < 8 * gpr) {
       const int64_t sr = src ? (int64_t)src[r] : (int64_t)r;
       if (sr >= 0 && sr < n_src) {
@@ -131,7 +136,7 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int e = u * 256 + threadIdx.x;
-    const uint32_t r = by * kRqRows + e / PPR, cp = bx * PPR + e % PPR;
+    const uint32_t r = by * ROWS + e / PPR, cp = bx * PPR + e % PPR;
     if (r >= M || cp >= 8 * gpr) continue;
     const int64_t i = (int64_t)r * ppr_all + cp;
     const uint32_t sw = sd[u];
@@ -163,11 +168,14 @@ hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void*
                                     const int32_t* src, int64_t n_src, void* out, float* out_s, int64_t M, int64_t Kb,
                                     hipStream_t stream) {
   if (M == 0 || Kb == 0) return hipSuccess;
-  constexpr int U = kRqRows * 8 * kRqGroups / 256;
   const int64_t gpr = Kb / 64;
-  const int64_t gx = (gpr + kRqGroups - 1) / kRqGroups, gy = (M + kRqRows - 1) / kRqRows;
+  const int64_t gx = (gpr + kRqGroups - 1) / kRqGroups;
+  const bool small = gx * ((M + kRqRows - 1) / kRqRows) < 2 * (int64_t)current_device_caps().cus;
+  const int rows = small ? kRqRowsSmall : kRqRows;
+  const int64_t gy = (M + rows - 1) / rows;
   const bool a8 = (q_stride % 8 == 0) && ((reinterpret_cast<uintptr_t>(q) & 7) == 0);
-  auto kernel = a8 ? mxfp4_to_fp8_kernel<U, true> : mxfp4_to_fp8_kernel<U, false>;
+  auto kernel = small ? (a8 ? mxfp4_to_fp8_kernel<kRqRowsSmall, true> : mxfp4_to_fp8_kernel<kRqRowsSmall, false>)
+                      : (a8 ? mxfp4_to_fp8_kernel<kRqRows, true> : mxfp4_to_fp8_kernel<kRqRows, false>);
   return launch(kernel, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q), q_stride,
                      static_cast<const uint8_t*>(s), s_stride, src, n_src, static_cast<u32x4*>(out), out_s,
                      (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
