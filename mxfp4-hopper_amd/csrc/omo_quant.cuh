@@ -77,55 +77,6 @@ __device__ __forceinline__ uint32_t chunk_absmax_bits(const u32x4& d) {
   return max(m & 0xFFFFu, m >> 16);
 }
 
-// Column variant: one lane owns a whole 32-element block given as 16 packed
-// bf16 pairs (element 2j low, 2j+1 high). Returns the 16 code bytes.
-__device__ __forceinline__ u32x4 quant_block32_fast(const uint32_t (&p)[16], uint32_t amax_bits, float eps, int c_eps,
-                                                    uint32_t* byte) {
-  float xmax = bf16_to_f32(amax_bits);
-  int c = (int)(amax_bits >> 7) - 129 + ((amax_bits & 0x7Fu) > 64u ? 1 : 0);
-  c = c < -33 ? -33 : c;
-  c = (xmax > eps) ? c : c_eps;
-  *byte = (uint32_t)(c + 127);
-  const float y_s = exp2i(c);
-  u32x4 out;
-#pragma unroll
-  for (int w = 0; w < 4; w++) {
-    uint32_t r = 0;
-    r = cvt_pk_fp4<0>(r, p[4 * w + 0], y_s);
-    r = cvt_pk_fp4<1>(r, p[4 * w + 1], y_s);
-    r = cvt_pk_fp4<2>(r, p[4 * w + 2], y_s);
-    r = cvt_pk_fp4<3>(r, p[4 * w + 3], y_s);
-    out[w] = r;
-  }
-  return out;
-}
-
-__device__ __forceinline__ u32x4 quant_block32_ref(const uint32_t (&p)[16], float eps, float fp4_min, float fp4_max,
-                                                   uint32_t* byte) {
-  float amax = eps;
-#pragma unroll
-  for (int k = 0; k < 16; k++) {
-    amax = fmax_abs_bf16(amax, p[k]);
-    amax = fmax_abs_bf16(amax, p[k] >> 16);
-  }
-  float inv;
-  *byte = ref_scale(amax, fp4_max, &inv);
-  u32x4 out;
-#pragma unroll
-  for (int w = 0; w < 4; w++) {
-    uint32_t o = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t pk = p[4 * w + k];
-      float qx = fminf(fmaxf(bf16_to_f32(pk & 0xFFFFu) * inv, fp4_min), fp4_max);
-      float qy = fminf(fmaxf(bf16_to_f32(pk >> 16) * inv, fp4_min), fp4_max);
-      o |= (e2m1_from_f32_ref(qx) | (e2m1_from_f32_ref(qy) << 4)) << (8 * k);
-    }
-    out[w] = o;
-  }
-  return out;
-}
-
 // Host-side scale exponent for amax == eps (exact
 // ceil(log2(max(fl(eps/fp4_max), 1e-10f)))).
 static inline int host_c_eps(float eps, float fp4_max) {
