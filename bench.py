@@ -13,8 +13,8 @@ cfg1 quantize + dequantize round trip (4096 x 4096), the MoE-payload requant/deq
 expert-parallel payload rows against Megatron's cat/split composition, the
 MXFP4 moe_permute gather (alone and fused into the FP8 requant), the
 cfg5 MoE layer composite (all codec launches of one layer on 8 local experts),
-the dual-layout quantize (7168 x 18432) and the row -> col FP8 conversion,
-each as GB/s of algorithmic bytes or microseconds per call, and memory-only
+the dual-layout quantize (7168 x 18432), the row -> col FP8 conversion and
+the per-split row -> col FP8 of cfg5's routed rows alone, each as GB/s of algorithmic bytes or microseconds per call, and memory-only
 kernels over the headline buffers (the quantize's loads and stores without
 its arithmetic; streaming reads; streaming writes) as the practical bound.
 
@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (>= 3 to exceed the 256 MB cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="comma list of extra legs: dequant,cfg1,payload,ep_payload,permute,moe,dual,rowcol,"
+                    help="comma list of extra legs: dequant,cfg1,payload,ep_payload,permute,moe,msplit,dual,rowcol,"
                          "ceiling; 'headline' runs the headline quantize alone")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (known traffic) for counter calibration")
@@ -574,6 +574,40 @@ def main():
         out["row_to_col_fp8"] = {"workload": "MXFP4 rowwise -> FP8 columnwise 4096x7168",
                                  "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
                                  "us_per_launch": round(t / steps * 1e3, 2)}
+
+    if want("msplit"):
+        # cfg5's per-split row -> col FP8 alone (the moe leg runs it after the grouped weight
+        # quantize, whose written lines it inherits): the 16431 routed rows of experts 0-7 in
+        # their 8 ragged splits, rotating buffer sets.
+        c5 = wl.CFG5
+        m_e = wl.moe_routing(c5["tokens"], c5["n_experts"], c5["topk"], range(c5["local_experts"]), seed=5)
+        R, Hd = sum(m_e), c5["hidden"]
+        b = sum(wl.row_to_col_fp8_bytes(m, Hd) for m in m_e)
+        ms_sets = sets_for(b, 3)
+        lens6, offs6, soffs6, mx6 = (torch.tensor(v, dtype=torch.int32, device=dev) if i < 3 else v
+                                     for i, v in enumerate(_split_meta(m_e)))
+        srows6 = sum(-(-m // 128) for m in m_e)
+        x6 = wl.normal_bf16((R, Hd), seed=70, device=dev)
+        q6 = [torch.empty((R, Hd // 2), dtype=torch.uint8, device=dev) for _ in range(ms_sets)]
+        s6 = [torch.empty((R, Hd // 32), dtype=torch.uint8, device=dev) for _ in range(ms_sets)]
+        for i in range(ms_sets):
+            omo.omo_per_token_group_quant_fp4(x6, q6[i], s6[i], 32, 1e-10, -6.0, 6.0, False)
+        del x6
+        o6 = [torch.empty((R * Hd,), dtype=torch.uint8, device=dev) for _ in range(ms_sets)]
+        os6 = [torch.empty((srows6, Hd), dtype=torch.float32, device=dev) for _ in range(ms_sets)]
+
+        def msplit(i):
+            _abi.check(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(
+                q6[i].data_ptr(), R, Hd // 2, s6[i].data_ptr(), s6[i].numel(), o6[i].data_ptr(), o6[i].numel(),
+                os6[i].data_ptr(), os6[i].numel(), lens6.data_ptr(), offs6.data_ptr(), soffs6.data_ptr(), len(m_e),
+                mx6, 1e-10, cur()))
+        steps = max(50, args.steps // 10)
+        t, _ = time_launches(torch, msplit, ms_sets, steps, 10)
+        out["msplit_cfg5"] = {"workload": f"per-split MXFP4 row -> FP8 col alone, cfg5's {R} routed rows x {Hd} in "
+                                          f"{len(m_e)} splits ({min(m_e)}..{max(m_e)} rows)",
+                              "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
+                              "us_per_launch": round(t / steps * 1e3, 2)}
+        del q6, s6, o6, os6
 
     if want("permute"):
         # TE's moe_permute on an MXFP4 tensor at one rank's share: 4096 tokens routed top-8 of 64
