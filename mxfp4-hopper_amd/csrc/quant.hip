@@ -301,20 +301,22 @@ hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, 
   const DeviceCaps dc = current_device_caps();
   const bool aligned16 = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(s)) & 15) == 0;
   // Two-phase kernel when each workgroup's share (a multiple of 64 chunks,
-  // 16 B of scale bytes) is at least 8192 chunks (at 4096, 2048 x 4096 ran
-  // 5.48 us two-phase against 5.02 us one-pass; 4096 x 4096, a share of
-  // 8192, 8.15 against 8.79), fits its LDS in one round
-  // (4 B of codes + 1/4 B of scale per chunk), and fills its steps of 2048
-  // chunks to at least 95%. Measured where it does not: 16431 x 2048 (8.03
-  // steps per CU) and 16431 x 4096 (16.06) ran 6-8% slower two-phase than
-  // quant_rowwise_kernel, both in 9 / 17 steps and with the surplus chunks
-  // loaded alongside the first step (8 / 16 steps); several rounds per
-  // workgroup (alternating read and write phases) measured 6-12% slower.
+  // 16 B of scale bytes) is at least 6144 chunks (at 4096, 2048 x 4096 ran
+  // 5.48 us two-phase against 5.06 us one-pass; at 6144, 3072 x 4096 6.59
+  // against 7.15; 4096 x 4096, a share of 8192, 8.15 against 8.79), fits its
+  // LDS in one round (4 B of codes + 1/4 B of scale per chunk), and either
+  // fills its steps of 2048 chunks to at least 95% or takes at most four of
+  // them (2048 x 7168, 3.5 steps: 7.49 against 8.22). Measured where neither
+  // holds: 16431 x 2048 (8.03 steps per CU) and 16431 x 4096 (16.06) ran
+  // 6-8% slower two-phase than quant_rowwise_kernel, both in 9 / 17 steps and
+  // with the surplus chunks loaded alongside the first step (8 / 16 steps);
+  // several rounds per workgroup (alternating read and write phases) measured
+  // 6-12% slower.
   const int64_t share = ((a.nchunks + dc.cus - 1) / dc.cus + 63) / 64 * 64;
   const int64_t cap = (int64_t)dc.lds_per_workgroup * 4 / 17 / 64 * 64;
   const int64_t steps = (share + kPhThreads * kPhUnroll - 1) / (kPhThreads * kPhUnroll);
   const double fill = (double)a.nchunks / ((double)dc.cus * kPhThreads * kPhUnroll * (double)steps);
-  if (standard && aligned16 && share >= 8192 && share <= cap && fill >= 0.95) {
+  if (standard && aligned16 && share >= 6144 && share <= cap && (fill >= 0.95 || steps <= 4)) {
     const int round = (int)share;
     return launch(quant_phased_kernel, dim3((unsigned)dc.cus), dim3(kPhThreads), (size_t)round * 4 + round / 4,
                        stream, a, share, round);

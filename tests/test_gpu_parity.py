@@ -180,16 +180,17 @@ def test_cfg1_round_trip(oracle, dev):
     np.testing.assert_array_equal(bits_u16(y2).reshape(-1), ey)
 
 
-@pytest.mark.parametrize("case", ["domain_tiled", "partial_last_workgroup", "steps_below_95"])
+@pytest.mark.parametrize("case", ["domain_tiled", "partial_last_workgroup", "steps_below_95", "few_partial_steps"])
 def test_quant_two_phase_path(oracle, dev, case):
     """Shapes around the two-phase kernel (one LDS round per CU, then 16 B
-    stores; taken when a CU's share is one round of at least 4096 chunks
-    that fills its 2048-chunk steps to 95%). On a 256-CU device:
-    every bf16 value under every scale exponent plus the special blocks in
-    exactly 2 steps per CU; a share of 7 steps whose last workgroup ends
-    early with a scale-byte tail that is not a multiple of 16; and a share
-    of 8.03 steps, which takes the one-pass kernel. Outputs start as a
-    sentinel, so every byte must be written."""
+    stores; taken when a CU's share is one round of at least 6144 chunks
+    that fills its 2048-chunk steps to 95% or takes at most four of them).
+    On a 256-CU device: every bf16 value under every scale exponent plus
+    the special blocks in exactly 2 steps per CU; a share of 7 steps whose
+    last workgroup ends early with a scale-byte tail that is not a multiple
+    of 16; a share of 8.03 steps, which takes the one-pass kernel; and a
+    share of 3.5 steps (2048 x 7168), whose last step is half full. Outputs
+    start as a sentinel, so every byte must be written."""
     _say("quant two-phase", case)
     if case == "domain_tiled":
         dom, _ = domain_blocks()
@@ -200,10 +201,14 @@ def test_quant_two_phase_path(oracle, dev, case):
         shape = (5, 5865632)  # 3,666,020 chunks: 255 shares of 14,336 and one of 10,340
         g = torch.Generator().manual_seed(32)
         xb = bits_u16((torch.randn(shape, generator=g) * 1e-3).to(torch.bfloat16)).reshape(-1)
-    else:
+    elif case == "steps_below_95":
         shape = (16431, 2048)
         g = torch.Generator().manual_seed(31)
         xb = bits_u16((torch.randn(shape, generator=g) * 5).to(torch.bfloat16)).reshape(-1)
+    else:
+        shape = (2048, 7168)
+        g = torch.Generator().manual_seed(33)
+        xb = bits_u16((torch.randn(shape, generator=g) * 0.3).to(torch.bfloat16)).reshape(-1)
     omo = _omo()
     x = from_u16(xb, dev).view(shape)
     q = torch.full((xb.size // 2,), 0xAB, dtype=torch.uint8, device=dev)
