@@ -252,8 +252,10 @@ hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, 
   a.c_eps = host_c_eps(eps, 6.0f);
   // Payload rows (scales right after the codes, one stride) take the
   // two-phase kernel when rpw whole rows per workgroup give every CU a share
-  // of at least 4096 chunks that fits its LDS and fills the 2048-chunk steps
-  // to at least 95%, the conditions under which quant_phased_kernel wins.
+  // of at least 6144 chunks that fits its LDS and fills the 2048-chunk steps
+  // to at least 95% or takes at most four of them, the conditions under
+  // which quant_phased_kernel wins (2048 x 7168, 3.5 steps: 7.7 us against
+  // 9.3 one-pass).
   const int64_t stride = K / 32 * 17;
   const bool packed = q_stride == stride && s_stride == stride && static_cast<uint8_t*>(s) == a.q + K / 2;
   const bool aligned16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q)) & 15) == 0;
@@ -266,7 +268,7 @@ hipError_t launch_quant_rows(const void* x, void* q, int64_t q_stride, void* s, 
     const int64_t steps = (share + kPhThreads * kPhUnroll - 1) / (kPhThreads * kPhUnroll);
     const double fill = (double)(rows * cpr) / ((double)grid * kPhThreads * kPhUnroll * (double)steps);
     const int64_t lds = share * 4 + share / 4;
-    if (share >= 4096 && lds <= dc.lds_per_workgroup && fill >= 0.95 && grid >= dc.cus / 2) {
+    if (share >= 6144 && lds <= dc.lds_per_workgroup && (fill >= 0.95 || steps <= 4) && grid >= dc.cus / 2) {
       QuantArgs p;
       p.x = static_cast<const u32x4*>(x);
       p.q = nullptr;

@@ -753,7 +753,8 @@ def _payload(codes, scales):
 # 4096 x 7168, 4090 x 7168 (a ragged last workgroup) and 4096 x 2048 take the
 # two-phase payload kernel; the others the one-pass row kernel.
 @pytest.mark.parametrize("T,H,seed", [(1, 128, 1), (300, 7168, 2), (64, 2048, 3), (5, 128, 0), (0, 7168, 5),
-                                      (4096, 7168, 6), (4090, 7168, 7), (4096, 2048, 8), (4096, 2048, 0)])
+                                      (4096, 7168, 6), (4090, 7168, 7), (4096, 2048, 8), (4096, 2048, 0),
+                                      (2048, 7168, 9)])
 def test_payload_quant(oracle, dev, T, H, seed):
     """Quantize into payload rows == torch.cat of the unfused quantize outputs."""
     from omo_python_api.ep_payload import fp4_quantize_packed, join_payload
