@@ -17,6 +17,8 @@ the dual-layout quantize (7168 x 18432), the row -> col FP8 conversion and
 the per-split row -> col FP8 of cfg5's routed rows alone, each as GB/s of algorithmic bytes or microseconds per call, and memory-only
 kernels over the headline buffers (the quantize's loads and stores without
 its arithmetic; streaming reads; streaming writes) as the practical bound.
+On request only (--only floors): each bandwidth-bound codec kernel beside a
+memory-only copy of its own access pattern, the floor that pattern sets.
 
 The CPU baseline runs the oracle (a multithreaded C restatement of the
 reference kernels) on the host's cores for the headline quantize and, in the
@@ -49,7 +51,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="comma list of extra legs: dequant,cfg1,payload,ep_payload,permute,moe,msplit,dual,rowcol,"
-                         "ceiling; 'headline' runs the headline quantize alone")
+                         "ceiling,floors ('floors' runs only when named); 'headline' runs the headline "
+                         "quantize alone")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (known traffic) for counter calibration")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -210,6 +213,128 @@ def ceiling_leg(torch, args, dev, cur, xs, qs, ss, numel, qbytes, value):
         "two_phase_traffic_GB/s": res["two_phase_traffic"][0], "two_phase_traffic_us": res["two_phase_traffic"][1],
         "quant_frac_of_ceiling": round(value / best, 4),
         "read_stream_GB/s": res["read_stream"][0], "write_stream_GB/s": res["write_stream"][0]}
+
+
+def floors_leg(torch, args, dev, cur, lib, _abi, wl):
+    """Each bandwidth-bound codec kernel beside a memory-only copy of its own
+    access pattern (mxfp4-hopper_amd/ceiling/mem_floors.hip: the same loads,
+    stores, workgroup shape, order and LDS footprint, no arithmetic), on the
+    same buffers: the floor that pattern sets on this HBM."""
+    import ctypes
+    fl = ctypes.CDLL(os.path.join(ROOT, "mxfp4-hopper_amd", "lib", "libomo_ceiling.so"))
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    fl.omo_floor_dual.argtypes = [P, P, P, P, P, I64, I64, P]
+    fl.omo_floor_rowcol.argtypes = [P, P, P, P, I64, I64, P]
+    fl.omo_floor_msplit.argtypes = [P, P, P, P, I64, I64, P, P, P, I64, I64, I64, P]
+    fl.omo_floor_requant.argtypes = [P, P, P, P, I64, I64, P]
+    fl.omo_floor_dequant.argtypes = [P, P, P, I64, P]
+
+    def chk(rc, what):
+        if rc:
+            raise RuntimeError(f"{what} returned {rc}")
+
+    def pair(name, workload, nbytes, n_sets, product, floor, steps):
+        tp, _ = time_launches(torch, product, n_sets, steps, 10)
+        tf, _ = time_launches(torch, floor, n_sets, steps, 10)
+        up, uf = tp / steps * 1e3, tf / steps * 1e3
+        res[name] = {"workload": workload, "kernel_us": round(up, 2), "floor_us": round(uf, 2),
+                     "kernel_frac_of_floor": round(uf / up, 3), "floor_frac_of_peak": round(nbytes / (uf * 1e-6) / 8e12, 3)}
+
+    res = {}
+    # dual-layout quantize, cfg3 7168 x 18432
+    M, K = 7168, 18432
+    n = M * K
+    xd = [wl.heavy_tail_weights(M, K, seed=33 + i, device=dev) for i in range(2)]
+    od = [[torch.empty(b, dtype=torch.uint8, device=dev) for b in (n // 2, n // 32, n // 2, n // 32)] for _ in range(2)]
+    pair("dual", "dual-layout quantize 7168x18432 (quant_dual_super_kernel)", wl.dual_quant_bytes(n), 2,
+         lambda i: chk(lib.omo_hip_quant_mxfp4_dual(xd[i].data_ptr(), M, K, od[i][0].data_ptr(), n // 2,
+                                                    od[i][1].data_ptr(), n // 32, od[i][2].data_ptr(), n // 2,
+                                                    od[i][3].data_ptr(), n // 32, 1e-10, cur()), "dual"),
+         lambda i: chk(fl.omo_floor_dual(xd[i].data_ptr(), od[i][0].data_ptr(), od[i][1].data_ptr(),
+                                         od[i][2].data_ptr(), od[i][3].data_ptr(), M, K, cur()), "dual floor"),
+         max(20, args.steps // 50))
+    del xd, od
+    # the code-reading kernels at cfg4's 4096 x 7168 (dequant at 8192 x 7168)
+    M, N = 4096, 7168
+    n = M * N
+    b4 = wl.requant_fp8_bytes(n)
+    ns = sets_for(b4, 4)
+    x4 = wl.normal_bf16((M, N), seed=60, device=dev)
+    q4 = [torch.empty((M, N // 2), dtype=torch.uint8, device=dev) for _ in range(ns)]
+    s4 = [torch.empty((M, N // 32), dtype=torch.uint8, device=dev) for _ in range(ns)]
+    for i in range(ns):
+        chk(lib.omo_hip_per_token_group_quant_fp4(x4.data_ptr(), n, q4[i].data_ptr(), n // 2, s4[i].data_ptr(),
+                                                  n // 32, 32, 1e-10, -6.0, 6.0, 0, cur()), "quantize")
+    del x4
+    o4 = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(ns)]
+    os4 = [torch.empty(n // 128, dtype=torch.float32, device=dev) for _ in range(ns)]
+    steps = max(100, args.steps // 4)
+    pair("requant_fp8", "rowwise FP8 requant 4096x7168 (mxfp4_to_fp8_kernel)", b4, ns,
+         lambda i: chk(lib.omo_hip_per_token_Mxfp4ToFp8(q4[i].data_ptr(), M, N // 2, s4[i].data_ptr(), n // 32,
+                                                        o4[i].data_ptr(), n, os4[i].data_ptr(), n // 128, 128, 1e-10,
+                                                        -6.0, 6.0, 0, cur()), "requant"),
+         lambda i: chk(fl.omo_floor_requant(q4[i].data_ptr(), s4[i].data_ptr(), o4[i].data_ptr(), os4[i].data_ptr(), M,
+                                            N // 2, cur()), "requant floor"), steps)
+    pair("row_to_col_fp8", "row -> col FP8 4096x7168 (row_to_fp8_col_wide_kernel)", wl.row_to_col_fp8_bytes(M, N), ns,
+         lambda i: chk(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(q4[i].data_ptr(), M, N // 2, s4[i].data_ptr(), M,
+                                                                    N // 32, o4[i].data_ptr(), N, M,
+                                                                    os4[i].data_ptr(), M // 128, N, 1e-10, cur()),
+                       "row->col"),
+         lambda i: chk(fl.omo_floor_rowcol(q4[i].data_ptr(), s4[i].data_ptr(), o4[i].data_ptr(), os4[i].data_ptr(), M, N,
+                                           cur()), "row->col floor"), steps)
+    del q4, s4, o4, os4
+    # per split, cfg5's routed rows
+    c5 = wl.CFG5
+    m_e = wl.moe_routing(c5["tokens"], c5["n_experts"], c5["topk"], range(c5["local_experts"]), seed=5)
+    R, Hd = sum(m_e), c5["hidden"]
+    b5 = sum(wl.row_to_col_fp8_bytes(m, Hd) for m in m_e)
+    ns = sets_for(b5, 3)
+    lens, offs, soffs, mx = (torch.tensor(v, dtype=torch.int32, device=dev) if i < 3 else v
+                             for i, v in enumerate(_split_meta(m_e)))
+    srows = sum(-(-m // 128) for m in m_e)
+    x5 = wl.normal_bf16((R, Hd), seed=70, device=dev)
+    q5 = [torch.empty((R, Hd // 2), dtype=torch.uint8, device=dev) for _ in range(ns)]
+    s5 = [torch.empty((R, Hd // 32), dtype=torch.uint8, device=dev) for _ in range(ns)]
+    for i in range(ns):
+        chk(lib.omo_hip_per_token_group_quant_fp4(x5.data_ptr(), R * Hd, q5[i].data_ptr(), R * Hd // 2,
+                                                  s5[i].data_ptr(), R * Hd // 32, 32, 1e-10, -6.0, 6.0, 0, cur()),
+            "quantize")
+    del x5
+    o5 = [torch.empty(R * Hd, dtype=torch.uint8, device=dev) for _ in range(ns)]
+    os5 = [torch.empty((srows, Hd), dtype=torch.float32, device=dev) for _ in range(ns)]
+    pair("msplit", f"per-split row -> col FP8, cfg5's {R} rows in {len(m_e)} ragged splits "
+                   "(row_to_fp8_col_msplit_wide_kernel)", b5, ns,
+         lambda i: chk(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(
+             q5[i].data_ptr(), R, Hd // 2, s5[i].data_ptr(), s5[i].numel(), o5[i].data_ptr(), o5[i].numel(),
+             os5[i].data_ptr(), os5[i].numel(), lens.data_ptr(), offs.data_ptr(), soffs.data_ptr(), len(m_e), mx, 1e-10,
+             cur()), "msplit"),
+         lambda i: chk(fl.omo_floor_msplit(q5[i].data_ptr(), s5[i].data_ptr(), o5[i].data_ptr(), os5[i].data_ptr(), R,
+                                           Hd, lens.data_ptr(), offs.data_ptr(), soffs.data_ptr(), len(m_e), mx, srows,
+                                           cur()), "msplit floor"), max(50, args.steps // 10))
+    del q5, s5, o5, os5
+    # dequant, 8192 x 7168
+    M, N = 8192, 7168
+    n = M * N
+    bq = wl.dequant_bytes(n)
+    ns = sets_for(bq, 4)
+    x6 = wl.normal_bf16((M, N), seed=61, device=dev)
+    q6 = [torch.empty(n // 2, dtype=torch.uint8, device=dev) for _ in range(ns)]
+    s6 = [torch.empty(n // 32, dtype=torch.uint8, device=dev) for _ in range(ns)]
+    for i in range(ns):
+        chk(lib.omo_hip_per_token_group_quant_fp4(x6.data_ptr(), n, q6[i].data_ptr(), n // 2, s6[i].data_ptr(),
+                                                  n // 32, 32, 1e-10, -6.0, 6.0, 0, cur()), "quantize")
+    del x6
+    y6 = [torch.empty(n, dtype=torch.bfloat16, device=dev) for _ in range(ns)]
+    pair("dequant", "dequant 8192x7168 (dequant_bf16_kernel)", bq, ns,
+         lambda i: chk(lib.omo_hip_per_token_Mxfp4ToBf16_dequant(q6[i].data_ptr(), n // 2, s6[i].data_ptr(), n // 32,
+                                                                y6[i].data_ptr(), n, None, 0, 32, 1e-10, -6.0, 6.0,
+                                                                0, cur()), "dequant"),
+         lambda i: chk(fl.omo_floor_dequant(q6[i].data_ptr(), s6[i].data_ptr(), y6[i].data_ptr(), n // 8, cur()),
+                       "dequant floor"), max(100, args.steps // 4))
+    del q6, s6, y6
+    res["note"] = ("floor: a memory-only copy of the kernel's own access pattern (mxfp4-hopper_amd/ceiling/"
+                   "mem_floors.hip) on the same buffers; kernel_frac_of_floor = floor time / kernel time")
+    return res
 
 
 def main():
@@ -658,6 +783,12 @@ def main():
             out["memory_ceiling"] = ceiling_leg(torch, args, dev, cur, xs, qs, ss, numel, qbytes, value)
         except (OSError, RuntimeError) as e:  # an optional leg: report, never lose the bench line
             out["memory_ceiling"] = {"error": str(e)}
+
+    if "floors" in only:
+        try:
+            out["pattern_floors"] = floors_leg(torch, args, dev, cur, lib, _abi, wl)
+        except (OSError, RuntimeError) as e:
+            out["pattern_floors"] = {"error": str(e)}
 
     line = {
         "metric": METRIC,

@@ -1,0 +1,307 @@
+// Memory-only copies of the codec kernels whose time is set by their loads
+// and stores. Each kernel issues the global loads and stores of the product
+// kernel it is named after - the same addresses, widths, cache policies,
+// workgroup shape, workgroup order and LDS footprint (so the same residency)
+// - with the arithmetic replaced by XORs of the loaded data. The time of one
+// of these is the floor of its product kernel's access pattern on this HBM.
+// Built into libomo_ceiling.so for bench.py's floors leg; nothing in the
+// product calls them.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+typedef uint32_t fu32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t fu32x2 __attribute__((ext_vector_type(2)));
+
+namespace {
+
+// The product's XCD-contiguous workgroup order (csrc/omo_device.cuh).
+__device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t n) {
+  const uint32_t x = b & 7u, j = b >> 3, q = n >> 3, r = n & 7u;
+  return x * q + (x < r ? x : r) + j;
+}
+
+// ---- dual-layout quantize, four 64 x 256 tiles per workgroup (quant_dual_super_kernel)
+struct DualFloorSmem {
+  __attribute__((aligned(16))) uint8_t tile[64 * 512];
+  __attribute__((aligned(16))) uint32_t row_codes[2][64 * 32];
+  __attribute__((aligned(8))) uint8_t row_scales[2][64 * 8];
+};
+
+__device__ __forceinline__ void dual_floor_flush(const DualFloorSmem& sm, int buf, uint32_t* __restrict__ row_q,
+                                                 uint8_t* __restrict__ row_s, int64_t m0, int64_t k0, int64_t K) {
+  const int t = threadIdx.x, row = t >> 3, piece = t & 7;
+  const fu32x4 c = *reinterpret_cast<const fu32x4*>(&sm.row_codes[buf][row * 32 + 4 * piece]);
+  __builtin_nontemporal_store(c, reinterpret_cast<fu32x4*>(row_q + (m0 + row) * (K / 8) + k0 / 8 + 4 * piece));
+  if (t < 64) {
+    *reinterpret_cast<fu32x2*>(row_s + (m0 + t) * (K / 32) + k0 / 32) =
+        *reinterpret_cast<const fu32x2*>(&sm.row_scales[buf][t * 8]);
+  }
+}
+
+// M % 256 == 0, K % 256 == 0, 16 B aligned buffers (the shapes the bench uses).
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void dual_floor(
+    const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q, uint8_t* __restrict__ row_s,
+    uint8_t* __restrict__ col_q, uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms, int tiles,
+    int per_xcd) {
+  __shared__ DualFloorSmem sm;
+  const int b = blockIdx.x;
+  const int logical = (b % 8) * per_xcd + b / 8;
+  if (logical >= tiles) return;
+  const int t = threadIdx.x, r0 = t >> 5, cc = t & 31;
+  const int64_t m0s = (int64_t)(logical % tiles_ms) * 256, k0 = (int64_t)(logical / tiles_ms) * 256;
+  uint32_t acc = 0;
+  for (int st = 0; st < 4; st++) {
+    const int64_t m0 = m0s + 64 * st;
+    const int buf = st & 1;
+    const uint16_t* src = x + (m0 + r0) * K + k0 + cc * 8;
+    fu32x4 d[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) d[k] = __builtin_nontemporal_load(reinterpret_cast<const fu32x4*>(src + 16 * k * K));
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      *reinterpret_cast<fu32x4*>(sm.tile + (r0 + 16 * k) * 512 + ((cc ^ (k << 2)) * 16)) = d[k];
+      sm.row_codes[buf][(r0 + 16 * k) * 32 + cc] = d[k].x ^ d[k].y;
+      if ((t & 3) == 0) sm.row_scales[buf][(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)d[k].z;
+    }
+    if (st > 0) dual_floor_flush(sm, buf ^ 1, row_q, row_s, m0 - 64, k0, K);
+    __syncthreads();
+    acc ^= *reinterpret_cast<const uint32_t*>(sm.tile + ((t * 68) & 32764));
+    __syncthreads();
+  }
+  dual_floor_flush(sm, 1, row_q, row_s, m0s + 192, k0, K);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int c = (t >> 3) + 64 * j, piece = t & 7;
+    fu32x4 v = *reinterpret_cast<const fu32x4*>(sm.tile + c * 128 + 16 * piece);
+    v.x ^= acc;
+    *reinterpret_cast<fu32x4*>(col_q + (k0 + c) * (M / 2) + m0s / 2 + 16 * piece) = v;
+  }
+  if ((t & 1) == 0) {
+    const int c = 2 * (t >> 2) + ((t >> 1) & 1);
+    *reinterpret_cast<fu32x2*>(col_s + (k0 + c) * (M / 32) + m0s / 32) = fu32x2{acc, (uint32_t)c};
+  }
+}
+
+// ---- row -> col FP8, 128 x 256 tiles (row_to_fp8_col_wide_kernel, row_to_fp8_col_msplit_wide_kernel)
+constexpr int kWideSmemBytes = 128 * 160 + 8 * 128 * 4 + 8 * 128;  // the product's WideSmem
+
+// A lane's 16 bytes of one column at dst, stopping at rows_valid: the
+// product's store of a column piece (one 16 B store, or 8/4/2/1-byte pieces
+// at the end of a split).
+__device__ __forceinline__ void floor_piece(uint8_t* __restrict__ dst, const fu32x4& w, int r_base, int rows_valid) {
+  if (r_base + 16 <= rows_valid) {
+    memcpy(dst, &w, 16);
+  } else if (r_base < rows_valid) {
+    const int n = rows_valid - r_base;
+    int pos = 0;
+    if (n & 8) {
+      const fu32x2 h = {w[0], w[1]};
+      memcpy(dst, &h, 8);
+      pos = 8;
+    }
+    if (n & 4) {
+      const uint32_t v = w[2];
+      memcpy(dst + pos, &v, 4);
+      pos += 4;
+    }
+    if (n & 2) {
+      const uint16_t v = (uint16_t)w[3];
+      memcpy(dst + pos, &v, 2);
+      pos += 2;
+    }
+    if (n & 1) dst[pos] = (uint8_t)(w[3] >> 16);
+  }
+}
+
+// One tile: loads of code rows row0 .. row0 + rows_valid - 1 and their scale
+// bytes, the LDS staging, then eight 16 B column pieces and one scale-row
+// float per lane.
+template <bool RAGGED>
+__device__ __forceinline__ void wide_floor_tile(uint8_t* sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                int64_t N, int64_t row0, int rows_valid, int64_t col0,
+                                                float* __restrict__ out_s_row, uint8_t* __restrict__ obase,
+                                                int64_t cstride, bool line_nt) {
+  const int t = threadIdx.x;
+  fu32x4 cv[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
+    cv[k] = fu32x4{0u, 0u, 0u, 0u};
+    if (!RAGGED || r < rows_valid) cv[k] = *reinterpret_cast<const fu32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
+  }
+  fu32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
+  if (t < 128 && (!RAGGED || t < rows_valid)) sv = *reinterpret_cast<const fu32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int id = t + 256 * k;
+    *reinterpret_cast<fu32x4*>(sm + (id >> 3) * 160 + (id & 7) * 16) = cv[k];
+  }
+  if (t < 128) *reinterpret_cast<fu32x2*>(sm + 128 * 160 + t * 8) = sv;
+  __syncthreads();
+  const int qq = t & 7, cg = t >> 3;
+  fu32x4 w = *reinterpret_cast<const fu32x4*>(sm + (qq * 16 + cg) * 160 + 16 * (cg & 7));
+  w.y ^= *reinterpret_cast<const uint32_t*>(sm + 128 * 160 + 8 * (t & 127));
+  __builtin_nontemporal_store(__uint_as_float(w.x & 0x3FFFFFFFu), out_s_row + 8 * cg + qq);
+  uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const fu32x4 we = w ^ fu32x4{(uint32_t)e, 0u, 0u, 0u};
+    if (RAGGED && !line_nt) floor_piece(o + e * cstride, we, 16 * qq, rows_valid);
+    else __builtin_nontemporal_store(we, reinterpret_cast<fu32x4*>(o + e * cstride));
+  }
+}
+
+// Dense, M % 128 == 0, N % 256 == 0, 16 B aligned output.
+__global__ __launch_bounds__(256, 4) void rowcol_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                       uint8_t* __restrict__ out, float* __restrict__ out_s, int64_t M,
+                                                       int64_t N) {
+  __shared__ __attribute__((aligned(16))) uint8_t sm[kWideSmemBytes];
+  const uint32_t L = xcd_order(blockIdx.x, gridDim.x), gx = (uint32_t)(N / 256);
+  const int64_t bn = L % gx, bm = L / gx;
+  wide_floor_tile<false>(sm, q, s, N, bm * 128, 128, bn * 256, out_s + bm * N + bn * 256, out + bn * 256 * M + bm * 128,
+                         M, false);
+}
+
+// Per split, N % 256 == 0 (grid: split, row tile, column band).
+__global__ __launch_bounds__(256, 4) void msplit_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                       uint8_t* __restrict__ out, float* __restrict__ out_s,
+                                                       const int32_t* __restrict__ lens, const int32_t* __restrict__ offs,
+                                                       const int32_t* __restrict__ soffs, int64_t total_rows, int64_t N,
+                                                       int64_t out_s_rows, bool out_line) {
+  __shared__ __attribute__((aligned(16))) uint8_t sm[kWideSmemBytes];
+  const int64_t split = blockIdx.x, bm = blockIdx.y, bn = blockIdx.z;
+  const int64_t len = lens[split];
+  if (bm * 128 >= len) return;
+  const int64_t start = offs[split], sstart = soffs[split];
+  if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
+  const int rows_valid = (int)(len - bm * 128 < 128 ? len - bm * 128 : 128);
+  wide_floor_tile<true>(sm, q, s, N, start + bm * 128, rows_valid, bn * 256, out_s + (sstart + bm) * N + bn * 256,
+                        out + start * N + bn * 256 * len + bm * 128, len, out_line && len % 128 == 0);
+}
+
+// ---- rowwise FP8 requant, 32 rows x 4 groups of 128 elements (mxfp4_to_fp8_kernel<32, true>)
+__global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                     fu32x4* __restrict__ out, float* __restrict__ out_s, uint32_t M,
+                                                     uint32_t gpr, uint32_t gx) {
+  const uint32_t L = xcd_order(blockIdx.x, gridDim.x), bx = L % gx, by = L / gx;
+  const int64_t kb = 64 * (int64_t)gpr, ppr = 8 * (int64_t)gpr;
+  fu32x2 c[4];
+  uint32_t sd[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int e = u * 256 + threadIdx.x;
+    const uint32_t r = by * 32 + e / 32, cp = bx * 32 + e % 32;
+    if (r < M && cp < 8 * gpr) {
+      c[u] = *reinterpret_cast<const fu32x2*>(q + r * kb + 8 * (int64_t)cp);
+      sd[u] = *reinterpret_cast<const uint32_t*>(s + r * (kb / 16) + 4 * (cp >> 3));
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int e = u * 256 + threadIdx.x;
+    const uint32_t r = by * 32 + e / 32, cp = bx * 32 + e % 32;
+    if (r >= M || cp >= 8 * gpr) continue;
+    __builtin_nontemporal_store(fu32x4{c[u][0], c[u][1], sd[u], c[u][0] ^ sd[u]}, out + (int64_t)r * ppr + cp);
+    if ((cp & 7) == 0) out_s[(int64_t)(cp >> 3) * M + r] = __uint_as_float(sd[u] & 0x3FFFFFFFu);
+  }
+}
+
+// ---- dequant to bf16, four code dwords per lane (dequant_bf16_kernel<4>)
+__global__ __launch_bounds__(256) void dequant_floor(const uint32_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                     fu32x4* __restrict__ out, int64_t ndw) {
+  const int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  uint32_t c[4], sb[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int64_t i = base + (int64_t)u * 256;
+    if (i < ndw) {
+      c[u] = q[i];
+      sb[u] = s[i >> 2];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int64_t i = base + (int64_t)u * 256;
+    if (i < ndw) __builtin_nontemporal_store(fu32x4{c[u], sb[u], c[u] ^ sb[u], c[u] + sb[u]}, out + i);
+  }
+}
+
+int device_lds() {
+  int dev = 0, lds = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+    return 0;
+  return lds;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Dual-layout floor for x [M, K] bf16 (M % 256 == 0, K % 256 == 0): outputs as
+// the product's (row codes M*K/2, row scales M*K/32, column codes, column scales).
+__attribute__((visibility("default"))) int omo_floor_dual(const void* x, void* row_q, void* row_s, void* col_q,
+                                                          void* col_s, int64_t M, int64_t K, hipStream_t stream) {
+  if (M <= 0 || K <= 0 || M % 256 || K % 256) return -1;
+  const int tiles_ms = (int)(M / 256), tiles = (int)(tiles_ms * (K / 256)), per_xcd = (tiles + 7) / 8;
+  hipLaunchKernelGGL(dual_floor, dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream, static_cast<const uint16_t*>(x),
+                     static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s), static_cast<uint8_t*>(col_q),
+                     static_cast<uint8_t*>(col_s), M, K, tiles_ms, tiles, per_xcd);
+  return (int)hipGetLastError();
+}
+
+// Dense row -> col floor: codes [M, N/2], scales [M, N/32] -> [N, M] bytes and
+// [M/128, N] floats (M % 128 == 0, N % 256 == 0).
+__attribute__((visibility("default"))) int omo_floor_rowcol(const void* q, const void* s, void* out, float* out_s,
+                                                            int64_t M, int64_t N, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || M % 128 || N % 256) return -1;
+  hipLaunchKernelGGL(rowcol_floor, dim3((unsigned)((M / 128) * (N / 256))), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, M,
+                     N);
+  return (int)hipGetLastError();
+}
+
+// Per-split row -> col floor, the product launcher's grid and LDS reserve
+// (residency capped at four workgroups per CU); N % 256 == 0, metadata as the
+// product's (int32 device arrays).
+__attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const void* s, void* out, float* out_s,
+                                                            int64_t total_rows, int64_t N, const int32_t* lens,
+                                                            const int32_t* offs, const int32_t* soffs, int64_t nsplits,
+                                                            int64_t max_split_len, int64_t out_s_rows,
+                                                            hipStream_t stream) {
+  if (N <= 0 || N % 256 || nsplits <= 0 || nsplits > 65535 || max_split_len <= 0 || max_split_len > total_rows ||
+      (max_split_len + 127) / 128 > 65535 || N / 256 > 65535)
+    return -1;
+  const int per_wg = device_lds() / 4 - 2560;
+  const size_t reserve = per_wg > kWideSmemBytes ? (size_t)(per_wg - kWideSmemBytes) : 0;
+  const dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + 127) / 128), (unsigned)(N / 256));
+  hipLaunchKernelGGL(msplit_floor, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
+                     static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
+                     out_s_rows, (reinterpret_cast<uintptr_t>(out) & 127) == 0);
+  return (int)hipGetLastError();
+}
+
+// Rowwise FP8 requant floor: codes [M, Kb], scales [M, Kb/16] -> [M, 2 Kb]
+// bytes and [Kb/64, M] floats (Kb % 64 == 0, 8 B aligned codes).
+__attribute__((visibility("default"))) int omo_floor_requant(const void* q, const void* s, void* out, float* out_s,
+                                                             int64_t M, int64_t Kb, hipStream_t stream) {
+  if (M <= 0 || Kb <= 0 || Kb % 64 || M > 0x7FFFFFFF) return -1;
+  const int64_t gpr = Kb / 64, gx = (gpr + 3) / 4, gy = (M + 31) / 32;
+  hipLaunchKernelGGL(requant_floor, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q),
+                     static_cast<const uint8_t*>(s), static_cast<fu32x4*>(out), out_s, (uint32_t)M, (uint32_t)gpr,
+                     (uint32_t)gx);
+  return (int)hipGetLastError();
+}
+
+// Dequant floor: ndw code dwords (+ ndw/4 scale bytes) -> ndw x 16 B.
+__attribute__((visibility("default"))) int omo_floor_dequant(const void* q, const void* s, void* out, int64_t ndw,
+                                                             hipStream_t stream) {
+  if (ndw <= 0) return -1;
+  hipLaunchKernelGGL(dequant_floor, dim3((unsigned)((ndw + 1023) / 1024)), dim3(256), 0, stream,
+                     static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<fu32x4*>(out), ndw);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"
