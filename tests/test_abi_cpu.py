@@ -134,6 +134,30 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2 and "exactly one GPU" in r.stdout
 
 
+def test_bench_floor_library_exports_and_shape_checks():
+    # the memory-only kernels bench.py times beside the codec kernels: exported,
+    # and shapes they do not cover are refused on the host before any launch
+    lib = ctypes.CDLL(os.path.join(ROOT, "mxfp4-hopper_amd", "lib", "libomo_ceiling.so"))
+    for name in ["omo_ceiling_launch", "omo_floor_dual", "omo_floor_rowcol", "omo_floor_msplit", "omo_floor_requant",
+                 "omo_floor_dequant"]:
+        assert hasattr(lib, name), name
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    lib.omo_floor_dual.argtypes = [P, P, P, P, P, I64, I64, P]
+    lib.omo_floor_rowcol.argtypes = [P, P, P, P, I64, I64, P]
+    lib.omo_floor_msplit.argtypes = [P, P, P, P, I64, I64, P, P, P, I64, I64, I64, P]
+    lib.omo_floor_requant.argtypes = [P, P, P, P, I64, I64, P]
+    lib.omo_floor_dequant.argtypes = [P, P, P, I64, P]
+    assert lib.omo_floor_dual(None, None, None, None, None, 7168, 18432 + 32, None) == -1
+    assert lib.omo_floor_dual(None, None, None, None, None, 0, 256, None) == -1
+    assert lib.omo_floor_rowcol(None, None, None, None, 4096 + 64, 7168, None) == -1
+    assert lib.omo_floor_rowcol(None, None, None, None, 4096, 7168 + 128, None) == -1
+    assert lib.omo_floor_msplit(None, None, None, None, 100, 7168 + 128, None, None, None, 2, 60, 2, None) == -1
+    assert lib.omo_floor_msplit(None, None, None, None, 100, 7168, None, None, None, 2, 101, 2, None) == -1
+    assert lib.omo_floor_msplit(None, None, None, None, 100, 7168, None, None, None, 0, 60, 2, None) == -1
+    assert lib.omo_floor_requant(None, None, None, None, 4096, 3584 + 32, None) == -1
+    assert lib.omo_floor_dequant(None, None, None, 0, None) == -1
+
+
 def test_payload_validation_paths():
     lib = _lib()
     f = ctypes.c_void_p(0x1000)
