@@ -111,6 +111,8 @@ def omo_per_token_group_quant_fp4(input, output_q, output_s, group_size, eps, fp
     Reference: omo::omo_per_token_group_quant_fp4, code/kernel/per_token_quant_mxfp4.cu:387-487."""
     _check_input(input, "input")
     _check_input(output_q, "output_q")
+    if group_size <= 0:
+        raise RuntimeError(f"group_size must be positive, got {group_size}")
     _check_eq(input.numel() % group_size, 0, "input.numel() % group_size == 0")
     _check_eq(output_s.dim(), 2, "output_s.dim() == 2")
     _same_device(input, output_q, output_s)

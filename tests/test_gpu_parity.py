@@ -325,6 +325,27 @@ def test_to_fp8_rowwise_rejects_reference_invalid_shapes(dev):
         run_to_fp8(q, s, dev)
 
 
+def test_quant_binding_rejects_bad_arguments(dev):
+    """Host checks before any launch: group_size zero, a numel that is not a
+    multiple of group_size (code/kernel/per_token_quant_mxfp4.cu:396), a group
+    size other than 32, and undersized outputs raise; the outputs are untouched."""
+    import omo
+    _say("quant binding bad arguments")
+    x = torch.ones((4, 64), dtype=torch.bfloat16, device=dev)
+    q = torch.full((4, 32), 0xAB, dtype=torch.uint8, device=dev)
+    s = torch.full((4, 2), 0xCD, dtype=torch.uint8, device=dev)
+    with pytest.raises(RuntimeError, match="group_size must be positive"):
+        omo.omo_per_token_group_quant_fp4(x, q, s, 0, 1e-10, -6.0, 6.0, False)
+    with pytest.raises(RuntimeError):
+        omo.omo_per_token_group_quant_fp4(x[:, :40].contiguous(), q, s, 64, 1e-10, -6.0, 6.0, False)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        omo.omo_per_token_group_quant_fp4(x, q, s, 64, 1e-10, -6.0, 6.0, False)
+    with pytest.raises(RuntimeError):
+        omo.omo_per_token_group_quant_fp4(x, q[:2], s, 32, 1e-10, -6.0, 6.0, False)
+    torch.cuda.synchronize()
+    assert bool((q == 0xAB).all()) and bool((s == 0xCD).all())
+
+
 def test_to_fp8_rowwise_cfg4(oracle, dev):
     _say("to_fp8 cfg4 4096x7168")
     x = torch.randn((4096, 7168), generator=torch.Generator().manual_seed(44)).to(torch.bfloat16)
