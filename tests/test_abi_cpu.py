@@ -134,6 +134,35 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2 and "exactly one GPU" in r.stdout
 
 
+def test_last_error_is_per_thread():
+    # the failure message belongs to the calling thread: two threads failing
+    # different checks at once each read back their own message
+    import threading
+    lib = _lib()
+    P = ctypes.c_void_p
+    barrier = threading.Barrier(2)
+    got = {}
+
+    def fail_with(group_size, key):
+        for _ in range(200):
+            rc = lib.omo_hip_per_token_group_quant_fp4(P(1), 64, P(1), 32, P(1), 2, group_size, 1e-10, -6.0, 6.0, 0,
+                                                       None)
+            barrier.wait()
+            msg = lib.omo_hip_last_error()
+            barrier.wait()
+            got.setdefault(key, set()).add((rc, msg))
+
+    ts = [threading.Thread(target=fail_with, args=(0, "zero")), threading.Thread(target=fail_with, args=(64, "g64"))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert len(got["zero"]) == 1 and len(got["g64"]) == 1
+    (rc0, m0), = got["zero"]
+    (rc1, m1), = got["g64"]
+    assert b"positive" in m0 and b"must be 32" in m1 and rc0 != 0 and rc1 != 0
+
+
 def test_bench_floor_library_exports_and_shape_checks():
     # the memory-only kernels bench.py times beside the codec kernels: exported,
     # and shapes they do not cover are refused on the host before any launch
