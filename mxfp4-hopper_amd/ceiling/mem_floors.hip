@@ -116,8 +116,8 @@ __device__ __forceinline__ void floor_piece(uint8_t* __restrict__ dst, const fu3
 }
 
 // One tile: loads of code rows row0 .. row0 + rows_valid - 1 and their scale
-// bytes, the LDS staging, then eight 16 B column pieces and one scale-row
-// float per lane.
+// bytes (rows past rows_valid reload the last row, as the product does), the
+// LDS staging, then eight 16 B column pieces and one scale-row float per lane.
 template <bool RAGGED>
 __device__ __forceinline__ void wide_floor_tile(uint8_t* sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                 int64_t N, int64_t row0, int rows_valid, int64_t col0,
@@ -128,11 +128,17 @@ __device__ __forceinline__ void wide_floor_tile(uint8_t* sm, const uint8_t* __re
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
-    cv[k] = fu32x4{0u, 0u, 0u, 0u};
-    if (!RAGGED || r < rows_valid) cv[k] = *reinterpret_cast<const fu32x4*>(q + (row0 + r) * (N / 2) + col0 / 2 + c16 * 16);
+    const int rr = RAGGED ? min(r, rows_valid - 1) : r;
+    cv[k] = *reinterpret_cast<const fu32x4*>(q + (row0 + rr) * (N / 2) + col0 / 2 + c16 * 16);
   }
   fu32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
-  if (t < 128 && (!RAGGED || t < rows_valid)) sv = *reinterpret_cast<const fu32x2*>(s + (row0 + t) * (N / 32) + col0 / 32);
+  if (t < 128) sv = *reinterpret_cast<const fu32x2*>(s + (row0 + (RAGGED ? min(t, rows_valid - 1) : t)) * (N / 32) + col0 / 32);
+  if (RAGGED) {
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (((t + 256 * k) >> 3) >= rows_valid) cv[k] = fu32x4{0u, 0u, 0u, 0u};
+    if (t >= rows_valid) sv = fu32x2{0x7F7F7F7Fu, 0x7F7F7F7Fu};
+  }
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int id = t + 256 * k;
@@ -175,6 +181,54 @@ __global__ __launch_bounds__(256, 4) void msplit_floor(const uint8_t* __restrict
   const int64_t len = lens[split];
   if (bm * 128 >= len) return;
   const int64_t start = offs[split], sstart = soffs[split];
+  if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
+  const int rows_valid = (int)(len - bm * 128 < 128 ? len - bm * 128 : 128);
+  wide_floor_tile<true>(sm, q, s, N, start + bm * 128, rows_valid, bn * 256, out_s + (sstart + bm) * N + bn * 256,
+                        out + start * N + bn * 256 * len + bm * 128, len, out_line && len % 128 == 0);
+}
+
+// Per split on the product's flat grid (at most 64 splits): real tiles
+// numbered split by split, band by band, row tile fastest, spread over the
+// XCDs in contiguous ranges; workgroups past the last real tile exit.
+__device__ __forceinline__ int wave_prefix(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
+__global__ __launch_bounds__(256, 4) void msplit_flat_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                            uint8_t* __restrict__ out, float* __restrict__ out_s,
+                                                            const int32_t* __restrict__ lens,
+                                                            const int32_t* __restrict__ offs,
+                                                            const int32_t* __restrict__ soffs, int64_t total_rows,
+                                                            int64_t N, int64_t out_s_rows, bool out_line, int nsplits,
+                                                            int tm, int bands) {
+  __shared__ __attribute__((aligned(16))) uint8_t sm[kWideSmemBytes];
+  const int lane = (int)(threadIdx.x & 63);
+  int len_l = 0, start_l = 0, sstart_l = 0;
+  if (lane < nsplits) {
+    len_l = lens[lane];
+    start_l = offs[lane];
+    sstart_l = soffs[lane];
+  }
+  const int tiles_l = len_l > 0 ? (int)min(((int64_t)len_l + 127) / 128, (int64_t)tm) : 0;
+  const int incl = wave_prefix(tiles_l), excl = incl - tiles_l;
+  const uint32_t n_real = (uint32_t)__builtin_amdgcn_readlane(incl, 63) * (uint32_t)bands;
+  if (blockIdx.x >= n_real) return;
+  const uint32_t L = xcd_order(blockIdx.x, n_real);
+  const uint64_t hit =
+      __ballot(tiles_l > 0 && L >= (uint32_t)bands * (uint32_t)excl && L < (uint32_t)bands * (uint32_t)incl);
+  const int i = (int)__builtin_ctzll(hit);
+  const uint32_t ti = (uint32_t)__builtin_amdgcn_readlane(tiles_l, i);
+  const uint32_t r = L - (uint32_t)bands * (uint32_t)__builtin_amdgcn_readlane(excl, i);
+  const int64_t bm = r % ti, bn = r / ti;
+  const int64_t len = __builtin_amdgcn_readlane(len_l, i), start = __builtin_amdgcn_readlane(start_l, i),
+                sstart = __builtin_amdgcn_readlane(sstart_l, i);
+  if (bm * 128 >= len) return;
   if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
   const int rows_valid = (int)(len - bm * 128 < 128 ? len - bm * 128 : 128);
   wide_floor_tile<true>(sm, q, s, N, start + bm * 128, rows_valid, bn * 256, out_s + (sstart + bm) * N + bn * 256,
@@ -263,9 +317,10 @@ __attribute__((visibility("default"))) int omo_floor_rowcol(const void* q, const
   return (int)hipGetLastError();
 }
 
-// Per-split row -> col floor, the product launcher's grid and LDS reserve
-// (residency capped at four workgroups per CU); N % 256 == 0, metadata as the
-// product's (int32 device arrays).
+// Per-split row -> col floor, the product launcher's grid (flat for at most
+// 64 splits, else split x row tile x band) and LDS reserve (residency capped
+// at four workgroups per CU); N % 256 == 0, metadata as the product's (int32
+// device arrays).
 __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const void* s, void* out, float* out_s,
                                                             int64_t total_rows, int64_t N, const int32_t* lens,
                                                             const int32_t* offs, const int32_t* soffs, int64_t nsplits,
@@ -276,7 +331,15 @@ __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const
     return -1;
   const int per_wg = device_lds() / 4 - 2560;
   const size_t reserve = per_wg > kWideSmemBytes ? (size_t)(per_wg - kWideSmemBytes) : 0;
-  const dim3 grid((unsigned)nsplits, (unsigned)((max_split_len + 127) / 128), (unsigned)(N / 256));
+  const int64_t tm = (max_split_len + 127) / 128, bands = N / 256;
+  if (nsplits <= 64 && nsplits * tm * bands < ((int64_t)1 << 31)) {
+    hipLaunchKernelGGL(msplit_flat_floor, dim3((unsigned)(nsplits * tm * bands)), dim3(256), reserve, stream,
+                       static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
+                       lens, offs, soffs, total_rows, N, out_s_rows, (reinterpret_cast<uintptr_t>(out) & 127) == 0,
+                       (int)nsplits, (int)tm, (int)bands);
+    return (int)hipGetLastError();
+  }
+  const dim3 grid((unsigned)nsplits, (unsigned)tm, (unsigned)bands);
   hipLaunchKernelGGL(msplit_floor, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
                      out_s_rows, (reinterpret_cast<uintptr_t>(out) & 127) == 0);

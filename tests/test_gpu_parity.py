@@ -634,6 +634,66 @@ def test_row_to_fp8_col_msplit_many_splits(oracle, dev, nsplits, N, seed):
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
+@pytest.mark.parametrize("nsplits,seed", [(1, 11), (2, 12), (7, 13), (16, 14), (33, 15), (64, 16), (65, 17)])
+def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed):
+    """Split counts on both sides of 64 (the flat grid's limit; 65 takes the
+    3-D grid) with very uneven lengths (empty, one-row, ragged and long
+    splits), N = 512 (two 256-column bands), into sentinel-filled outputs."""
+    rng = np.random.default_rng(seed)
+    splits = [int(v) for v in rng.choice([0, 1, 17, 127, 128, 129, 300, 700, 1500], size=nsplits)]
+    if sum(splits) == 0:
+        splits[-1] = 129
+    N = 512
+    _say("msplit uneven split counts", nsplits, sum(splits))
+    q, s = payload_from_normal(sum(splits), N, seed)
+    got, got_s = _msplit_sentinel_run(dev, q, s, splits, N)
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(got, eo)
+    np.testing.assert_array_equal(got_s, es.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,extra", [(512, 0), (512, 66), (384, 0)])
+def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
+    """Split metadata is read on the device, so the kernels skip tiles whose
+    rows or scale rows fall outside the buffers: a split running past the
+    last row, one whose scale rows start past output_s, and one with a
+    negative row offset leave nothing written, and the valid splits around
+    them convert normally. Every buffer is a view inside a larger sentinel-
+    filled allocation, so a tile that were not skipped would land in the
+    padding (checked untouched) instead of outside the allocation. N = 512
+    takes the flat grid (extra = 66 adds empty splits: the 3-D grid), N = 384
+    the 128-column kernel."""
+    import omo
+    _say("msplit bad metadata", N, extra)
+    valid = [300, 129]
+    M = sum(valid)
+    srows = sum((m + 127) // 128 for m in valid)
+    lens = [300, 200, 129, 128, 64] + [0] * extra
+    offs = [0, M - 100, 300, 0, -5] + [0] * extra
+    soffs = [0, 0, 3, srows, 0] + [0] * extra
+    q, s = payload_from_normal(M, N, 5)
+    pad = 256
+    big_q = torch.zeros((M + 2 * pad, N // 2), dtype=torch.uint8, device=dev)
+    big_s = torch.full((M + 2 * pad, N // 32), 127, dtype=torch.uint8, device=dev)
+    big_q[pad:pad + M] = torch.from_numpy(q).to(dev)
+    big_s[pad:pad + M] = torch.from_numpy(s).to(dev)
+    big_out = torch.full(((M + 2 * pad) * N,), 0xAB, dtype=torch.uint8, device=dev)
+    big_os = torch.full((srows + 2 * 4, N), float("nan"), dtype=torch.float32, device=dev)
+    out_q = big_out[pad * N:(pad + M) * N].view(FP8)
+    out_s = big_os[4:4 + srows]
+    meta = [torch.tensor(v, dtype=torch.int32, device=dev) for v in (lens, offs, soffs)]
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(big_q[pad:pad + M], big_s[pad:pad + M], out_q, out_s, *meta, 300,
+                                                    1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, valid)
+    np.testing.assert_array_equal(bits_u8(out_q), eo)
+    np.testing.assert_array_equal(out_s.cpu().numpy().view(np.uint32), es.view(np.uint32))
+    out_all = bits_u8(big_out)
+    assert (out_all[:pad * N] == 0xAB).all() and (out_all[(pad + M) * N:] == 0xAB).all()
+    os_all = big_os.cpu().numpy()
+    assert np.isnan(os_all[:4]).all() and np.isnan(os_all[4 + srows:]).all()
+
+
 @pytest.mark.parametrize("N", [256, 1056])
 def test_row_to_fp8_col_msplit_short_max_len(oracle, dev, N):
     """The reference launches ceil(max_split_len / 128) row tiles per split
