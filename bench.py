@@ -303,7 +303,7 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
     o5 = [torch.empty(R * Hd, dtype=torch.uint8, device=dev) for _ in range(ns)]
     os5 = [torch.empty((srows, Hd), dtype=torch.float32, device=dev) for _ in range(ns)]
     pair("msplit", f"per-split row -> col FP8, cfg5's {R} rows in {len(m_e)} ragged splits "
-                   "(row_to_fp8_col_msplit_wide_kernel)", b5, ns,
+                   "(row_to_fp8_col_msplit_flat_kernel)", b5, ns,
          lambda i: chk(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(
              q5[i].data_ptr(), R, Hd // 2, s5[i].data_ptr(), s5[i].numel(), o5[i].data_ptr(), o5[i].numel(),
              os5[i].data_ptr(), os5[i].numel(), lens.data_ptr(), offs.data_ptr(), soffs.data_ptr(), len(m_e), mx, 1e-10,
