@@ -244,13 +244,12 @@ __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__
   fu32x2 c[4];
   uint32_t sd[4];
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
+  for (int u = 0; u < 4; u++) {  // unconditional loads at clamped indices, as the product issues them
     const int e = u * 256 + threadIdx.x;
     const uint32_t r = by * 32 + e / 32, cp = bx * 32 + e % 32;
-    if (r < M && cp < 8 * gpr) {
-      c[u] = *reinterpret_cast<const fu32x2*>(q + r * kb + 8 * (int64_t)cp);
-      sd[u] = *reinterpret_cast<const uint32_t*>(s + r * (kb / 16) + 4 * (cp >> 3));
-    }
+    const uint32_t rr = r < M ? r : M - 1, cpc = cp < 8 * gpr ? cp : 8 * gpr - 1;
+    c[u] = *reinterpret_cast<const fu32x2*>(q + rr * kb + 8 * (int64_t)cpc);
+    sd[u] = *reinterpret_cast<const uint32_t*>(s + rr * (kb / 16) + 4 * (cpc >> 3));
   }
 #pragma unroll
   for (int u = 0; u < 4; u++) {
