@@ -803,50 +803,79 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
   return v;
 }
 
-// Per split on a flat grid, for at most 64 splits. The tiles that hold rows
+// Per split on a flat grid, for at most 128 splits. The tiles that hold rows
 // (ceil(len_i / 128) row tiles of split i, at most the grid's tm, times the
 // column bands) are numbered split by split, band by band, row tile fastest,
 // and spread over the XCDs in contiguous ranges: every XCD gets the same
 // number of real tiles, and the two tiles that share a column's 128 B output
 // lines (row tiles bm and bm + 1) run next to each other on one XCD, where
 // their partial lines merge in L2. Each wave finds its workgroup's tile
-// itself: lane i reads split i's metadata, a wave sum gives the tile
-// numbering, a ballot the split. Workgroups past the last real tile exit.
+// itself: lane l reads the metadata of splits l + 64k, wave sums give the
+// tile numbering, a ballot the split. Workgroups past the last real tile
+// exit.
 // On the 3-D grid (split, row tile, band) a split's tiles all land on one
 // XCD when the split count is a multiple of 8 (the XCD holding the longest
 // splits then finishes last) and are scattered otherwise. On 16431 routed
-// rows x 7168 with the same tile code, the flat grid took 52.4-56.1 us for
-// 4, 6, 7, 8, 12, 16 and 32 splits, the 3-D grid 54.7 us for cfg5's 8 nearly
-// equal splits and 72-174 us for uneven ones.
-constexpr int kFlatMaxSplits = 64;
+// rows x 7168 with the same tile code, the flat grid took 52.2-56.1 us for 4
+// to 65 splits of any balance and 57.6 and 62.0 us for 100 and 128 splits;
+// the 3-D grid 54.7 us for cfg5's 8 nearly equal splits, 72-174 us for 4 to
+// 32 uneven ones and 70-74 us for 65 to 128. Past 128 splits the 3-D grid is
+// kept: hundreds of short splits balance by their number, and four metadata
+// chunks per lane lost there (77.7 against 76.1 us at 200 splits, 82.1
+// against 77.4 at 256).
+constexpr int kFlatMaxSplits = 128;  // lane l of each wave holds splits l and l + 64
 
+template <int CHUNKS>  // splits per lane: 1 (up to 64 splits) or 2 (up to 128)
 __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
     int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool out_line, int nsplits, int tm, int bands) {
   __shared__ WideSmem sm;
   const int lane = (int)(threadIdx.x & 63);
-  int len_l = 0, start_l = 0, sstart_l = 0;
-  if (lane < nsplits) {
-    len_l = lens[lane];
-    start_l = offs[lane];
-    sstart_l = soffs[lane];
+  int len_l[CHUNKS], start_l[CHUNKS], sstart_l[CHUNKS];
+#pragma unroll
+  for (int k = 0; k < CHUNKS; k++) {
+    const int j = lane + 64 * k;
+    len_l[k] = start_l[k] = sstart_l[k] = 0;
+    if (j < nsplits) {
+      len_l[k] = lens[j];
+      start_l[k] = offs[j];
+      sstart_l[k] = soffs[j];
+    }
   }
-  const int tiles_l = len_l > 0 ? (int)min(((int64_t)len_l + kTile - 1) / kTile, (int64_t)tm) : 0;
-  const int incl = wave_inclusive_sum(tiles_l);
-  const int excl = incl - tiles_l;
+  // tiles of each split, numbered in split order: chunk k's splits follow
+  // the tiles of chunks 0 .. k-1
+  int tiles_l[CHUNKS], lo_l[CHUNKS], hi_l[CHUNKS];
+  uint32_t before = 0;
+#pragma unroll
+  for (int k = 0; k < CHUNKS; k++) {
+    tiles_l[k] = len_l[k] > 0 ? (int)min(((int64_t)len_l[k] + kTile - 1) / kTile, (int64_t)tm) : 0;
+    const int incl = wave_inclusive_sum(tiles_l[k]);
+    lo_l[k] = (int)before + incl - tiles_l[k];
+    hi_l[k] = (int)before + incl;
+    before += (uint32_t)__builtin_amdgcn_readlane(incl, 63);
+  }
   // real tiles: at most nsplits * tm * bands, the grid size (below 2^31)
-  const uint32_t n_real = (uint32_t)__builtin_amdgcn_readlane(incl, 63) * (uint32_t)bands;
+  const uint32_t n_real = before * (uint32_t)bands;
   if (blockIdx.x >= n_real) return;
   const uint32_t L = xcd_contiguous(blockIdx.x, n_real);
-  // exactly one split's range [bands * excl, bands * incl) holds L
-  const uint64_t hit =
-      __ballot(tiles_l > 0 && L >= (uint32_t)bands * (uint32_t)excl && L < (uint32_t)bands * (uint32_t)incl);
-  const int i = (int)__builtin_ctzll(hit);
-  const uint32_t ti = (uint32_t)__builtin_amdgcn_readlane(tiles_l, i);
-  const uint32_t r = L - (uint32_t)bands * (uint32_t)__builtin_amdgcn_readlane(excl, i);
-  msplit_wide_tile(sm, q, s, out, out_s, __builtin_amdgcn_readlane(len_l, i), __builtin_amdgcn_readlane(start_l, i),
-                   __builtin_amdgcn_readlane(sstart_l, i), r % ti, r / ti, total_rows, N, out_s_rows, eps, out_line);
+  // exactly one split's range [bands * lo, bands * hi) holds L
+  int64_t len = 0, start = 0, sstart = 0;
+  uint32_t ti = 1, r = 0;
+#pragma unroll
+  for (int k = 0; k < CHUNKS; k++) {
+    const uint64_t hit = __ballot(tiles_l[k] > 0 && L >= (uint32_t)bands * (uint32_t)lo_l[k] &&
+                                  L < (uint32_t)bands * (uint32_t)hi_l[k]);
+    if (hit) {
+      const int i = (int)__builtin_ctzll(hit);
+      ti = (uint32_t)__builtin_amdgcn_readlane(tiles_l[k], i);
+      r = L - (uint32_t)bands * (uint32_t)__builtin_amdgcn_readlane(lo_l[k], i);
+      len = __builtin_amdgcn_readlane(len_l[k], i);
+      start = __builtin_amdgcn_readlane(start_l[k], i);
+      sstart = __builtin_amdgcn_readlane(sstart_l[k], i);
+    }
+  }
+  msplit_wide_tile(sm, q, s, out, out_s, len, start, sstart, r % ti, r / ti, total_rows, N, out_s_rows, eps, out_line);
 }
 
 // A split's output column c is a run of len bytes at off*N + c*len, so a
@@ -926,7 +955,8 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   const bool out_line = (reinterpret_cast<uintptr_t>(out) & 127) == 0;
   if (wide && nsplits <= kFlatMaxSplits && nsplits * tiles_m * bands < ((int64_t)1 << 31)) {
     const dim3 grid((unsigned)(nsplits * tiles_m * bands));
-    return launch(row_to_fp8_col_msplit_flat_kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
+    auto kernel = nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1> : row_to_fp8_col_msplit_flat_kernel<2>;
+    return launch(kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
                   static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
                   out_s_rows, eps, out_line, (int)nsplits, (int)tiles_m, (int)bands);
   }

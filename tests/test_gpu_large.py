@@ -150,12 +150,12 @@ def _msplit_gpu(dev, q, s, splits):
     return out, outs
 
 
-@pytest.mark.parametrize("empty_tail", [0, 64])
+@pytest.mark.parametrize("empty_tail", [0, 255])
 def test_msplit_more_row_tiles_than_grid_y(oracle, dev, empty_tail):
     """A split of 8,400,037 rows has 65,626 row tiles, past the 65,536 that
-    grid y holds: with two splits the flat grid covers them, and with 64
-    empty splits appended (66 splits, past the flat grid's 64) the 3-D launch
-    is split over row-tile ranges. Row windows at the start, across tile
+    grid y holds: with two splits the flat grid covers them, and with 255
+    empty splits appended (257 splits, past the flat grid's 128) the 3-D
+    launch is split over row-tile ranges. Row windows at the start, across tile
     65,535 and at the end against the oracle."""
     splits, N = [8_400_037, 300] + [0] * empty_tail, 256
     R = sum(splits)
@@ -173,10 +173,10 @@ def test_msplit_more_row_tiles_than_grid_y(oracle, dev, empty_tail):
     np.testing.assert_array_equal(outs[-es.shape[0]:].cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
-@pytest.mark.parametrize("N,empty_tail", [(65536 * 256 + 256, 0), (65536 * 256 + 256, 64), (65536 * 128 + 128, 0)])
+@pytest.mark.parametrize("N,empty_tail", [(65536 * 256 + 256, 0), (65536 * 256 + 256, 255), (65536 * 128 + 128, 0)])
 def test_msplit_more_column_bands_than_grid_z(oracle, dev, N, empty_tail):
     """Rows of 16.8M (256-column bands, the wide kernel: on the flat grid,
-    and with 64 empty splits appended on the 3-D grid) or 8.4M columns
+    and with 255 empty splits appended on the 3-D grid) or 8.4M columns
     (128-column bands, the general kernel) have more than the 65,536 column
     bands grid z holds: column windows at the start and across the last band
     boundaries against the oracle on those columns."""

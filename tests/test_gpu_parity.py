@@ -634,11 +634,13 @@ def test_row_to_fp8_col_msplit_many_splits(oracle, dev, nsplits, N, seed):
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
-@pytest.mark.parametrize("nsplits,seed", [(1, 11), (2, 12), (7, 13), (16, 14), (33, 15), (64, 16), (65, 17)])
+@pytest.mark.parametrize("nsplits,seed", [(1, 11), (2, 12), (7, 13), (16, 14), (33, 15), (64, 16), (65, 17),
+                                          (128, 18), (129, 19), (256, 20)])
 def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed):
-    """Split counts on both sides of 64 (the flat grid's limit; 65 takes the
-    3-D grid) with very uneven lengths (empty, one-row, ragged and long
-    splits), N = 512 (two 256-column bands), into sentinel-filled outputs."""
+    """Split counts on both sides of 64 (one split per lane on the flat grid)
+    and of 128 (the flat grid's limit; 129 and 256 take the 3-D grid) with
+    very uneven lengths (empty, one-row, ragged and long splits), N = 512
+    (two 256-column bands), into sentinel-filled outputs."""
     rng = np.random.default_rng(seed)
     splits = [int(v) for v in rng.choice([0, 1, 17, 127, 128, 129, 300, 700, 1500], size=nsplits)]
     if sum(splits) == 0:
@@ -652,7 +654,7 @@ def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed):
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
-@pytest.mark.parametrize("N,extra", [(512, 0), (512, 66), (384, 0)])
+@pytest.mark.parametrize("N,extra", [(512, 0), (512, 66), (512, 260), (384, 0)])
 def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
     """Split metadata is read on the device, so the kernels skip tiles whose
     rows or scale rows fall outside the buffers: a split running past the
@@ -661,8 +663,8 @@ def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
     them convert normally. Every buffer is a view inside a larger sentinel-
     filled allocation, so a tile that were not skipped would land in the
     padding (checked untouched) instead of outside the allocation. N = 512
-    takes the flat grid (extra = 66 adds empty splits: the 3-D grid), N = 384
-    the 128-column kernel."""
+    takes the flat grid (extra empty splits: two splits per lane at 66, the
+    3-D grid at 260), N = 384 the 128-column kernel."""
     import omo
     _say("msplit bad metadata", N, extra)
     valid = [300, 129]
