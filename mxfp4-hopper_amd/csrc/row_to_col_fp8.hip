@@ -825,12 +825,13 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
 // against 77.4 at 256).
 constexpr int kFlatMaxSplits = 128;  // lane l of each wave holds splits l and l + 64
 
+// The tile of this workgroup on the flat grid: split, row tile bm and band
+// bn, or false past the last real tile (uniform over the workgroup).
 template <int CHUNKS>  // splits per lane: 1 (up to 64 splits) or 2 (up to 128)
-__global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
-    const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
-    const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
-    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool out_line, int nsplits, int tm, int bands) {
-  __shared__ WideSmem sm;
+__device__ __forceinline__ bool flat_split_tile(const int32_t* __restrict__ lens, const int32_t* __restrict__ offs,
+                                                const int32_t* __restrict__ soffs, int nsplits, int tm, int bands,
+                                                int64_t* len, int64_t* start, int64_t* sstart, int64_t* bm,
+                                                int64_t* bn) {
   const int lane = (int)(threadIdx.x & 63);
   int len_l[CHUNKS], start_l[CHUNKS], sstart_l[CHUNKS];
 #pragma unroll
@@ -857,11 +858,11 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
   }
   // real tiles: at most nsplits * tm * bands, the grid size (below 2^31)
   const uint32_t n_real = before * (uint32_t)bands;
-  if (blockIdx.x >= n_real) return;
+  if (blockIdx.x >= n_real) return false;
   const uint32_t L = xcd_contiguous(blockIdx.x, n_real);
   // exactly one split's range [bands * lo, bands * hi) holds L
-  int64_t len = 0, start = 0, sstart = 0;
   uint32_t ti = 1, r = 0;
+  *len = *start = *sstart = 0;
 #pragma unroll
   for (int k = 0; k < CHUNKS; k++) {
     const uint64_t hit = __ballot(tiles_l[k] > 0 && L >= (uint32_t)bands * (uint32_t)lo_l[k] &&
@@ -870,12 +871,25 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
       const int i = (int)__builtin_ctzll(hit);
       ti = (uint32_t)__builtin_amdgcn_readlane(tiles_l[k], i);
       r = L - (uint32_t)bands * (uint32_t)__builtin_amdgcn_readlane(lo_l[k], i);
-      len = __builtin_amdgcn_readlane(len_l[k], i);
-      start = __builtin_amdgcn_readlane(start_l[k], i);
-      sstart = __builtin_amdgcn_readlane(sstart_l[k], i);
+      *len = __builtin_amdgcn_readlane(len_l[k], i);
+      *start = __builtin_amdgcn_readlane(start_l[k], i);
+      *sstart = __builtin_amdgcn_readlane(sstart_l[k], i);
     }
   }
-  msplit_wide_tile(sm, q, s, out, out_s, len, start, sstart, r % ti, r / ti, total_rows, N, out_s_rows, eps, out_line);
+  *bm = r % ti;
+  *bn = r / ti;
+  return true;
+}
+
+template <int CHUNKS>
+__global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
+    const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
+    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool out_line, int nsplits, int tm, int bands) {
+  __shared__ WideSmem sm;
+  int64_t len, start, sstart, bm, bn;
+  if (!flat_split_tile<CHUNKS>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn)) return;
+  msplit_wide_tile(sm, q, s, out, out_s, len, start, sstart, bm, bn, total_rows, N, out_s_rows, eps, out_line);
 }
 
 // A split's output column c is a run of len bytes at off*N + c*len, so a
@@ -884,15 +898,14 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
 // store whatever the alignment (a previous version staged the pieces in LDS
 // and wrote aligned 16 B blocks plus partial edge blocks; ragged cfg5 splits
 // took 86.7 us that way against 60.8 us now, the same as 16-aligned splits).
-__global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
-    const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
-    const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
-    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs, int64_t bm0, int64_t bn0) {
-  __shared__ RowColSmem sm;
-  const int64_t split = blockIdx.x, bm = bm0 + blockIdx.y, bn = bn0 + blockIdx.z;
-  const int64_t len = lens[split];
+// Row tile bm, 128-column band bn of a split (rows [start, start + len),
+// scale rows from sstart), with the metadata checks of the wide form.
+__device__ __forceinline__ void msplit_narrow_tile(RowColSmem& sm, const uint8_t* __restrict__ q,
+                                                   const uint8_t* __restrict__ s, uint8_t* __restrict__ out,
+                                                   float* __restrict__ out_s, int64_t len, int64_t start,
+                                                   int64_t sstart, int64_t bm, int64_t bn, int64_t total_rows,
+                                                   int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs) {
   if (bm * kTile >= len) return;
-  const int64_t start = offs[split], sstart = soffs[split];
   // Metadata arrives on the device; tiles whose rows or scale rows fall
   // outside the buffers are skipped rather than written out of bounds.
   if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
@@ -909,6 +922,35 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
     rc_store(out + o0, res.e0, 16 * qq, rows_valid);
     rc_store(out + o0 + len, res.e1, 16 * qq, rows_valid);
   }
+}
+
+__global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
+    const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
+    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs, int64_t bm0, int64_t bn0) {
+  __shared__ RowColSmem sm;
+  const int64_t split = blockIdx.x, bm = bm0 + blockIdx.y, bn = bn0 + blockIdx.z;
+  const int64_t len = lens[split];
+  if (bm * kTile >= len) return;
+  msplit_narrow_tile(sm, q, s, out, out_s, len, offs[split], soffs[split], bm, bn, total_rows, N, out_s_rows, eps, vin,
+                     vs);
+}
+
+// The 128-column tiles on the flat grid (at most 128 splits), as the wide
+// form. On 16431 routed rows x 7040 columns: 4, 16 and 32 uneven splits
+// 71.4, 96.2 and 85.8 us against 94.1, 313.3 and 177.7 us on the 3-D grid;
+// cfg5's 8 nearly equal splits 71.3 against 65.8 us (the tile search of
+// twice as many 512-thread workgroups costs more than the 3-D grid's one
+// split per XCD, which any imbalance above about 8% undoes).
+template <int CHUNKS>
+__global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_narrow_flat_kernel(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
+    const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
+    int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs, int nsplits, int tm, int bands) {
+  __shared__ RowColSmem sm;
+  int64_t len, start, sstart, bm, bn;
+  if (!flat_split_tile<CHUNKS>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn)) return;
+  msplit_narrow_tile(sm, q, s, out, out_s, len, start, sstart, bm, bn, total_rows, N, out_s_rows, eps, vin, vs);
 }
 
 hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t N, float eps,
@@ -953,12 +995,18 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   const int per_wg = current_device_caps().lds_per_workgroup / 4 - 2560;
   const size_t reserve = per_wg > (int)sizeof(WideSmem) ? (size_t)(per_wg - (int)sizeof(WideSmem)) : 0;
   const bool out_line = (reinterpret_cast<uintptr_t>(out) & 127) == 0;
-  if (wide && nsplits <= kFlatMaxSplits && nsplits * tiles_m * bands < ((int64_t)1 << 31)) {
+  if (nsplits <= kFlatMaxSplits && nsplits * tiles_m * bands < ((int64_t)1 << 31)) {
     const dim3 grid((unsigned)(nsplits * tiles_m * bands));
-    auto kernel = nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1> : row_to_fp8_col_msplit_flat_kernel<2>;
-    return launch(kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
+    if (wide) {
+      auto kernel = nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1> : row_to_fp8_col_msplit_flat_kernel<2>;
+      return launch(kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
+                    static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
+                    out_s_rows, eps, out_line, (int)nsplits, (int)tiles_m, (int)bands);
+    }
+    auto kernel = nsplits <= 64 ? row_to_fp8_col_msplit_narrow_flat_kernel<1> : row_to_fp8_col_msplit_narrow_flat_kernel<2>;
+    return launch(kernel, grid, dim3(kRcThreads), 0, stream, static_cast<const uint8_t*>(q),
                   static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
-                  out_s_rows, eps, out_line, (int)nsplits, (int)tiles_m, (int)bands);
+                  out_s_rows, eps, vin, vs, (int)nsplits, (int)tiles_m, (int)bands);
   }
   // Grid y (row tiles) and z (column bands) hold at most 65536 each: longer
   // splits or wider rows take several launches over offset ranges.

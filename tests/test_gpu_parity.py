@@ -634,18 +634,19 @@ def test_row_to_fp8_col_msplit_many_splits(oracle, dev, nsplits, N, seed):
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
-@pytest.mark.parametrize("nsplits,seed", [(1, 11), (2, 12), (7, 13), (16, 14), (33, 15), (64, 16), (65, 17),
-                                          (128, 18), (129, 19), (256, 20)])
-def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed):
+@pytest.mark.parametrize("nsplits,seed,N", [(1, 11, 512), (2, 12, 512), (7, 13, 512), (16, 14, 512), (33, 15, 512),
+                                            (64, 16, 512), (65, 17, 512), (128, 18, 512), (129, 19, 512),
+                                            (256, 20, 512), (16, 21, 384), (100, 22, 384), (129, 23, 384)])
+def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed, N):
     """Split counts on both sides of 64 (one split per lane on the flat grid)
     and of 128 (the flat grid's limit; 129 and 256 take the 3-D grid) with
-    very uneven lengths (empty, one-row, ragged and long splits), N = 512
-    (two 256-column bands), into sentinel-filled outputs."""
+    very uneven lengths (empty, one-row, ragged and long splits), into
+    sentinel-filled outputs: N = 512 (two 256-column bands), N = 384 (three
+    bands of the 128-column kernel)."""
     rng = np.random.default_rng(seed)
     splits = [int(v) for v in rng.choice([0, 1, 17, 127, 128, 129, 300, 700, 1500], size=nsplits)]
     if sum(splits) == 0:
         splits[-1] = 129
-    N = 512
     _say("msplit uneven split counts", nsplits, sum(splits))
     q, s = payload_from_normal(sum(splits), N, seed)
     got, got_s = _msplit_sentinel_run(dev, q, s, splits, N)
@@ -654,7 +655,7 @@ def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed):
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
-@pytest.mark.parametrize("N,extra", [(512, 0), (512, 66), (512, 260), (384, 0)])
+@pytest.mark.parametrize("N,extra", [(512, 0), (512, 66), (512, 260), (384, 0), (384, 260)])
 def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
     """Split metadata is read on the device, so the kernels skip tiles whose
     rows or scale rows fall outside the buffers: a split running past the
@@ -664,7 +665,7 @@ def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
     filled allocation, so a tile that were not skipped would land in the
     padding (checked untouched) instead of outside the allocation. N = 512
     takes the flat grid (extra empty splits: two splits per lane at 66, the
-    3-D grid at 260), N = 384 the 128-column kernel."""
+    3-D grid at 260), N = 384 the 128-column kernel (flat, and 3-D at 260)."""
     import omo
     _say("msplit bad metadata", N, extra)
     valid = [300, 129]
