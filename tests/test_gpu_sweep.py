@@ -138,7 +138,11 @@ class Sweep:
     def msplit(self):
         from omo_python_api.mxfp4_dequant import split_metadata
         r = self.rng
-        if r.random() < 0.5:
+        u = r.random()
+        if u < 0.3:  # many splits: two per lane on the flat grid, past 128 the 3-D grid
+            splits = [int(v) for v in r.integers(0, 300, size=int(r.integers(60, 141)))]
+            N = int(r.choice([128, 256])) * int(r.integers(1, 4))
+        elif u < 0.65:
             splits, N = [int(v) for v in r.integers(0, 400, size=int(r.integers(1, 12)))], 128 * int(r.integers(1, 8))
         else:
             splits, N = [int(v) for v in r.integers(0, 700, size=int(r.integers(1, 10)))], 256 * int(r.integers(1, 8))
