@@ -235,26 +235,26 @@ __global__ __launch_bounds__(256, 4) void msplit_flat_floor(const uint8_t* __res
                         out + start * N + bn * 256 * len + bm * 128, len, out_line && len % 128 == 0);
 }
 
-// ---- rowwise FP8 requant, 32 rows x 4 groups of 128 elements (mxfp4_to_fp8_kernel<32, true>)
+// ---- rowwise FP8 requant, 16 rows x 4 groups of 128 elements (mxfp4_to_fp8_kernel<16, true>)
 __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                      fu32x4* __restrict__ out, float* __restrict__ out_s, uint32_t M,
                                                      uint32_t gpr, uint32_t gx) {
   const uint32_t L = xcd_order(blockIdx.x, gridDim.x), bx = L % gx, by = L / gx;
   const int64_t kb = 64 * (int64_t)gpr, ppr = 8 * (int64_t)gpr;
-  fu32x2 c[4];
-  uint32_t sd[4];
+  fu32x2 c[2];
+  uint32_t sd[2];
 #pragma unroll
-  for (int u = 0; u < 4; u++) {  // unconditional loads at clamped indices, as the product issues them
+  for (int u = 0; u < 2; u++) {  // unconditional loads at clamped indices: the pattern's best case
     const int e = u * 256 + threadIdx.x;
-    const uint32_t r = by * 32 + e / 32, cp = bx * 32 + e % 32;
+    const uint32_t r = by * 16 + e / 32, cp = bx * 32 + e % 32;
     const uint32_t rr = r < M ? r : M - 1, cpc = cp < 8 * gpr ? cp : 8 * gpr - 1;
     c[u] = *reinterpret_cast<const fu32x2*>(q + rr * kb + 8 * (int64_t)cpc);
     sd[u] = *reinterpret_cast<const uint32_t*>(s + rr * (kb / 16) + 4 * (cpc >> 3));
   }
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
+  for (int u = 0; u < 2; u++) {
     const int e = u * 256 + threadIdx.x;
-    const uint32_t r = by * 32 + e / 32, cp = bx * 32 + e % 32;
+    const uint32_t r = by * 16 + e / 32, cp = bx * 32 + e % 32;
     if (r >= M || cp >= 8 * gpr) continue;
     __builtin_nontemporal_store(fu32x4{c[u][0], c[u][1], sd[u], c[u][0] ^ sd[u]}, out + (int64_t)r * ppr + cp);
     if ((cp & 7) == 0) out_s[(int64_t)(cp >> 3) * M + r] = __uint_as_float(sd[u] & 0x3FFFFFFFu);
@@ -350,7 +350,7 @@ __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const
 __attribute__((visibility("default"))) int omo_floor_requant(const void* q, const void* s, void* out, float* out_s,
                                                              int64_t M, int64_t Kb, hipStream_t stream) {
   if (M <= 0 || Kb <= 0 || Kb % 64 || M > 0x7FFFFFFF) return -1;
-  const int64_t gpr = Kb / 64, gx = (gpr + 3) / 4, gy = (M + 31) / 32;
+  const int64_t gpr = Kb / 64, gx = (gpr + 3) / 4, gy = (M + 15) / 16;
   hipLaunchKernelGGL(requant_floor, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<fu32x4*>(out), out_s, (uint32_t)M, (uint32_t)gpr,
                      (uint32_t)gx);

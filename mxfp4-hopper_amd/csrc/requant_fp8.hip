@@ -83,12 +83,14 @@ __device__ __forceinline__ u32x2 to_fp8_dword_ref(uint32_t c, uint32_t offset) {
 // of it is assembled from partial writes of several workgroups on different
 // XCDs. FP8 bytes are written non-temporally; codes are read with ordinary
 // loads (non-temporal code loads made this kernel and the transposed one
-// 15-16% slower). Inputs of few rows take 8-row tiles instead (ROWS), so that
-// a launch still spreads over the CUs: 128 x 7168 ran 3.2 us in 56 tiles of
-// 32 rows; its scale runs are then 32 B pieces of lines that four
+// 15-16% slower). The tile height (ROWS) is 16 rows without a gather and 32
+// with one (the launcher says why); inputs of few rows take 8-row tiles, so
+// that a launch still spreads over the CUs: 128 x 7168 ran 3.2 us in 56 tiles
+// of 32 rows; its scale runs are then 32 B pieces of lines that four
 // workgroups share.
 constexpr int kRqGroups = 4;
 constexpr int kRqRows = 32;
+constexpr int kRqRowsPlain = 16;
 constexpr int kRqRowsSmall = 8;
 // Codes of row r start at q + r * q_stride and its scale bytes at
 // s + r * s_stride (bytes): contiguous [M, Kb] + [M, Kb/16] tensors, or the
@@ -171,11 +173,16 @@ hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void*
   const int64_t gpr = Kb / 64;
   const int64_t gx = (gpr + kRqGroups - 1) / kRqGroups;
   const bool small = gx * ((M + kRqRows - 1) / kRqRows) < 2 * (int64_t)current_device_caps().cus;
-  const int rows = small ? kRqRowsSmall : kRqRows;
+  // Without a gather, 16-row tiles (two pairs per lane, twice the workgroups)
+  // hide more of the conversion: 4096 x 7168 7.99 against 8.15 us. With one,
+  // the 32-row tiles keep four gathered rows' loads in flight per lane: the
+  // gathered requant of 32868 rows 50.4 against 53.1 us with 16-row tiles.
+  const int rows = small ? kRqRowsSmall : (src ? kRqRows : kRqRowsPlain);
   const int64_t gy = (M + rows - 1) / rows;
   const bool a8 = (q_stride % 8 == 0) && ((reinterpret_cast<uintptr_t>(q) & 7) == 0);
-  auto kernel = small ? (a8 ? mxfp4_to_fp8_kernel<kRqRowsSmall, true> : mxfp4_to_fp8_kernel<kRqRowsSmall, false>)
-                      : (a8 ? mxfp4_to_fp8_kernel<kRqRows, true> : mxfp4_to_fp8_kernel<kRqRows, false>);
+  auto kernel = rows == kRqRowsSmall ? (a8 ? mxfp4_to_fp8_kernel<kRqRowsSmall, true> : mxfp4_to_fp8_kernel<kRqRowsSmall, false>)
+                : rows == kRqRowsPlain ? (a8 ? mxfp4_to_fp8_kernel<kRqRowsPlain, true> : mxfp4_to_fp8_kernel<kRqRowsPlain, false>)
+                                       : (a8 ? mxfp4_to_fp8_kernel<kRqRows, true> : mxfp4_to_fp8_kernel<kRqRows, false>);
   return launch(kernel, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q), q_stride,
                      static_cast<const uint8_t*>(s), s_stride, src, n_src, static_cast<u32x4*>(out), out_s,
                      (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
