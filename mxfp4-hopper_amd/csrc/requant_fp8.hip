@@ -74,14 +74,15 @@ __device__ __forceinline__ u32x2 to_fp8_dword_ref(uint32_t c, uint32_t offset) {
   return o;
 }
 
-// Block tile: kRqRows rows x kRqGroups groups of 128 elements (256 code
-// bytes per row, 8 KiB per block). Lane e of the tile (e = u * 256 + t)
-// converts code pair c = e % (8 kRqGroups) of tile row e / (8 kRqGroups):
-// 16 B stores, contiguous over 16-lane row pieces. The fp32 scales of a tile
-// land in kRqGroups runs of kRqRows consecutive floats of the transposed
-// scale tensor [K/128, M], each written whole by one block, so no 128 B line
-// of it is assembled from partial writes of several workgroups on different
-// XCDs. FP8 bytes are written non-temporally; codes are read with ordinary
+// Block tile: ROWS rows x kRqGroups groups of 128 elements (256 code bytes
+// per row). Lane e of the tile (e = u * 256 + t) converts code pair
+// c = e % (8 kRqGroups) of tile row e / (8 kRqGroups): 16 B stores,
+// contiguous over 16-lane row pieces. The fp32 scales of a tile land in
+// kRqGroups runs of ROWS consecutive floats of the transposed scale tensor
+// [K/128, M]: a whole 128 B line with 32-row tiles, half of one with 16-row
+// tiles, whose other half comes from the next row tile, placed on the same
+// XCD by the contiguous renumbering below, so no line is assembled from
+// partial writes on different XCDs. FP8 bytes are written non-temporally; codes are read with ordinary
 // loads (non-temporal code loads made this kernel and the transposed one
 // 15-16% slower). The tile height (ROWS) is 16 rows without a gather and 32
 // with one (the launcher says why); inputs of few rows take 8-row tiles, so
