@@ -316,10 +316,11 @@ __attribute__((visibility("default"))) int omo_floor_rowcol(const void* q, const
   return (int)hipGetLastError();
 }
 
-// Per-split row -> col floor, the product launcher's grid (flat for at most
-// 64 splits, else split x row tile x band) and LDS reserve (residency capped
-// at four workgroups per CU); N % 256 == 0, metadata as the product's (int32
-// device arrays).
+// Per-split row -> col floor with the product launcher's LDS reserve
+// (residency capped at four workgroups per CU); N % 256 == 0, metadata as the
+// product's (int32 device arrays). Its flat grid reads one split per lane, so
+// it takes at most 64 splits (split x row tile x band beyond): it matches the
+// product's grid only up to 64 splits (the product's flat grid takes 128).
 __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const void* s, void* out, float* out_s,
                                                             int64_t total_rows, int64_t N, const int32_t* lens,
                                                             const int32_t* offs, const int32_t* soffs, int64_t nsplits,
@@ -331,7 +332,7 @@ __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const
   const int per_wg = device_lds() / 4 - 2560;
   const size_t reserve = per_wg > kWideSmemBytes ? (size_t)(per_wg - kWideSmemBytes) : 0;
   const int64_t tm = (max_split_len + 127) / 128, bands = N / 256;
-  if (nsplits <= 64 && nsplits * tm * bands < ((int64_t)1 << 31)) {
+  if (nsplits <= 64 && tm * bands <= (int64_t)UINT32_MAX / 256 / nsplits) {
     hipLaunchKernelGGL(msplit_flat_floor, dim3((unsigned)(nsplits * tm * bands)), dim3(256), reserve, stream,
                        static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
                        lens, offs, soffs, total_rows, N, out_s_rows, (reinterpret_cast<uintptr_t>(out) & 127) == 0,

@@ -995,7 +995,10 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   const int per_wg = current_device_caps().lds_per_workgroup / 4 - 2560;
   const size_t reserve = per_wg > (int)sizeof(WideSmem) ? (size_t)(per_wg - (int)sizeof(WideSmem)) : 0;
   const bool out_line = (reinterpret_cast<uintptr_t>(out) & 127) == 0;
-  if (nsplits <= kFlatMaxSplits && nsplits * tiles_m * bands < ((int64_t)1 << 31)) {
+  // A launch holds at most 2^32 - 1 work-items along x (gridDim.x times the
+  // workgroup size), so the flat grid's limit depends on the kernel's width.
+  const int64_t flat_threads = wide ? 256 : kRcThreads;
+  if (nsplits <= kFlatMaxSplits && tiles_m * bands <= (int64_t)UINT32_MAX / flat_threads / nsplits) {
     const dim3 grid((unsigned)(nsplits * tiles_m * bands));
     if (wide) {
       auto kernel = nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1> : row_to_fp8_col_msplit_flat_kernel<2>;

@@ -656,7 +656,12 @@ def bind_to_te(te_quantizer=None, te_quantized_tensor=None, te_quantized_tensor_
     ``QuantizedTensor`` from ``transformer_engine.pytorch.tensor.quantized_tensor``,
     ``QuantizedTensorBase`` from the same module where it exists); an
     ImportError means TE is not installed and the restated classes above are
-    the ones to use."""
+    the ones to use.
+
+    One set of bases per process: the registered names are what pickles
+    record, so a second binding on other bases would make the first family's
+    instances unpicklable; it raises RuntimeError instead. Loading a pickled
+    TE-bound tensor in a new process needs bind_to_te() to have run first."""
     if te_quantizer is None or te_quantized_tensor is None:
         from transformer_engine.pytorch.tensor import quantized_tensor as _te_qt  # noqa: F401
         te_quantizer = te_quantizer or _te_qt.Quantizer
@@ -665,6 +670,9 @@ def bind_to_te(te_quantizer=None, te_quantized_tensor=None, te_quantized_tensor_
             te_quantized_tensor_base = getattr(_te_qt, "QuantizedTensorBase", None)
     key = (te_quantizer, te_quantized_tensor, te_quantized_tensor_base)
     if key not in _TE_BOUND:
+        if _TE_BOUND:
+            raise RuntimeError("bind_to_te: the TE-bound MXFP4 classes already exist on other base classes; "
+                               "their registered names (TEMXFP4Tensor, ...) can name only one family per process")
         _TE_BOUND[key] = build_mxfp4_classes(te_quantizer, te_quantized_tensor, te_quantized_tensor_base or object,
                                              name_prefix="TE")
     return _TE_BOUND[key]

@@ -173,13 +173,17 @@ def test_msplit_more_row_tiles_than_grid_y(oracle, dev, empty_tail):
     np.testing.assert_array_equal(outs[-es.shape[0]:].cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
-@pytest.mark.parametrize("N,empty_tail", [(65536 * 256 + 256, 0), (65536 * 256 + 256, 255), (65536 * 128 + 128, 0)])
+@pytest.mark.parametrize("N,empty_tail", [(65536 * 256 + 256, 0), (65536 * 256 + 256, 255), (65536 * 128 + 128, 0),
+                                          (65536 * 128 + 128, 125)])
 def test_msplit_more_column_bands_than_grid_z(oracle, dev, N, empty_tail):
     """Rows of 16.8M (256-column bands, the wide kernel: on the flat grid,
     and with 255 empty splits appended on the 3-D grid) or 8.4M columns
     (128-column bands, the general kernel) have more than the 65,536 column
     bands grid z holds: column windows at the start and across the last band
-    boundaries against the oracle on those columns."""
+    boundaries against the oracle on those columns. With 125 empty splits
+    appended (128 splits, the flat grid's limit) the 128-column flat grid
+    would need 128 x 65,537 workgroups of 512 lanes, past the 2^32 - 1
+    work-items a launch holds along x, so the 3-D grid takes it."""
     splits = [128, 1, 77] + [0] * empty_tail
     R = sum(splits)
     _say("msplit wide rows", splits, N)

@@ -223,6 +223,25 @@ def test_bind_to_te_bases():
     assert not isinstance(mx.MXFP4Quantizer(), te.Quantizer)
 
 
+def test_bind_to_te_refuses_other_bases():
+    """A second binding on different bases would re-register TEMXFP4Tensor and
+    break pickling of the first family's instances: it raises, and the first
+    family still round-trips through pickle."""
+    mx = _mx()
+    te = _StandInTE
+    ns = mx.bind_to_te(te.Quantizer, te.QuantizedTensor, te.QuantizedTensorBase)
+
+    class OtherQuantizer(te.Quantizer):
+        pass
+
+    with pytest.raises(RuntimeError, match="already exist"):
+        mx.bind_to_te(OtherQuantizer, te.QuantizedTensor, te.QuantizedTensorBase)
+    assert mx.bind_to_te(te.Quantizer, te.QuantizedTensor, te.QuantizedTensorBase) is ns
+    t = ns.MXFP4Quantizer(rowwise=True, columnwise=False).make_empty((64, 32), dtype=torch.bfloat16, device="cpu")
+    s = pickle.loads(pickle.dumps(t))
+    assert type(s) is ns.MXFP4Tensor and torch.equal(s._rowwise_data, t._rowwise_data)
+
+
 def test_bind_to_te_without_te():
     """With no bases given the TE package is imported; it is absent here."""
     mx = _mx()
