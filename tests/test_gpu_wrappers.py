@@ -80,7 +80,7 @@ def test_to_fp8_wrapper_padding(oracle, dev, H, splits, seed):
     assert np.array_equal(bits_u8(qt), q) and np.array_equal(bits_u8(st), s)
 
 
-@pytest.mark.parametrize("M,H,seed", [(3, 128, 1), (130, 7168, 2), (64, 1152, 3)])
+@pytest.mark.parametrize("M,H,seed", [(2, 128, 1), (130, 7168, 2), (64, 1152, 3)])
 def test_to_bf16_to_fp8_wrapper(oracle, dev, M, H, seed):
     from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToBf16ToFp8_wrapper
     _say("ToBf16ToFp8 wrapper", M, H)
