@@ -219,7 +219,9 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
     """Each bandwidth-bound codec kernel beside a memory-only copy of its own
     access pattern (mxfp4-hopper_amd/ceiling/mem_floors.hip: the same loads,
     stores, workgroup shape, order and LDS footprint, no arithmetic), on the
-    same buffers: the floor that pattern sets on this HBM."""
+    same buffers: the floor that pattern sets on this HBM. Beside them,
+    memory-only copies of schedules the product does not use (alt): what a
+    different schedule of the same traffic would allow."""
     import ctypes
     fl = ctypes.CDLL(os.path.join(ROOT, "mxfp4-hopper_amd", "lib", "libomo_ceiling.so"))
     P, I64 = ctypes.c_void_p, ctypes.c_int64
@@ -228,6 +230,8 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
     fl.omo_floor_msplit.argtypes = [P, P, P, P, I64, I64, P, P, P, I64, I64, I64, P]
     fl.omo_floor_requant.argtypes = [P, P, P, P, I64, I64, P]
     fl.omo_floor_dequant.argtypes = [P, P, P, I64, P]
+    fl.omo_floor_dual_variant.argtypes = [ctypes.c_int, P, P, P, P, P, I64, I64, P]
+    fl.omo_floor_msplit_band.argtypes = [P, P, P, P, I64, P, P, P, I64, I64, P]
 
     def chk(rc, what):
         if rc:
@@ -239,6 +243,15 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
         up, uf = tp / steps * 1e3, tf / steps * 1e3
         res[name] = {"workload": workload, "kernel_us": round(up, 2), "floor_us": round(uf, 2),
                      "kernel_frac_of_floor": round(uf / up, 3), "floor_frac_of_peak": round(nbytes / (uf * 1e-6) / 8e12, 3)}
+
+    def alt(name, workload, nbytes, n_sets, floor, steps, against):
+        """A memory-only copy of a schedule the product does not use, timed on
+        the same buffers as `against`'s pair."""
+        tf, _ = time_launches(torch, floor, n_sets, steps, 10)
+        uf = tf / steps * 1e3
+        res[name] = {"workload": workload, "floor_us": round(uf, 2),
+                     "floor_frac_of_peak": round(nbytes / (uf * 1e-6) / 8e12, 3),
+                     "vs_product_floor": round(res[against]["floor_us"] / uf, 3)}
 
     res = {}
     # dual-layout quantize, cfg3 7168 x 18432
@@ -253,6 +266,17 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
          lambda i: chk(fl.omo_floor_dual(xd[i].data_ptr(), od[i][0].data_ptr(), od[i][1].data_ptr(),
                                          od[i][2].data_ptr(), od[i][3].data_ptr(), M, K, cur()), "dual floor"),
          max(20, args.steps // 50))
+    for kind, name, what in ((1, "dual_no_scale_stores", "the product's schedule without its scale stores (the bound "
+                                                         "of the code traffic; not a valid output)"),
+                             (2, "dual_scales_as_whole_lines", "the product's schedule with each workgroup's 4 KB of "
+                                                               "scale bytes stored as whole non-temporal lines "
+                                                               "(layout-free bound; not a valid output)"),
+                             (3, "dual_k_fastest", "the product's stores with super-tiles numbered K-fastest")):
+        alt(name, f"dual-layout floor 7168x18432: {what}", wl.dual_quant_bytes(n), 2,
+            lambda i, kind=kind: chk(fl.omo_floor_dual_variant(kind, xd[i].data_ptr(), od[i][0].data_ptr(),
+                                                               od[i][1].data_ptr(), od[i][2].data_ptr(),
+                                                               od[i][3].data_ptr(), M, K, cur()), "dual variant"),
+            max(20, args.steps // 50), "dual")
     del xd, od
     # the code-reading kernels at cfg4's 4096 x 7168 (dequant at 8192 x 7168)
     M, N = 4096, 7168
@@ -311,6 +335,12 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
          lambda i: chk(fl.omo_floor_msplit(q5[i].data_ptr(), s5[i].data_ptr(), o5[i].data_ptr(), os5[i].data_ptr(), R,
                                            Hd, lens.data_ptr(), offs.data_ptr(), soffs.data_ptr(), len(m_e), mx, srows,
                                            cur()), "msplit floor"), max(50, args.steps // 10))
+    alt("msplit_band_schedule", "per-split floor of the band schedule: one workgroup per (split, 64 columns) "
+        "staging the split's band in LDS and writing its contiguous [64 x len] output block in address order with "
+        "aligned non-temporal 16 B stores", b5, ns,
+        lambda i: chk(fl.omo_floor_msplit_band(q5[i].data_ptr(), s5[i].data_ptr(), o5[i].data_ptr(), os5[i].data_ptr(),
+                                               Hd, lens.data_ptr(), offs.data_ptr(), soffs.data_ptr(), len(m_e), mx,
+                                               cur()), "msplit band floor"), max(50, args.steps // 10), "msplit")
     del q5, s5, o5, os5
     # dequant, 8192 x 7168
     M, N = 8192, 7168

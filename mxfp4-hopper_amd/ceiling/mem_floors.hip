@@ -7,6 +7,8 @@
 // Built into libomo_ceiling.so for bench.py's floors leg; nothing in the
 // product calls them.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <stdint.h>
 #include <string.h>
 
@@ -33,13 +35,21 @@ __device__ __forceinline__ void dual_floor_flush(const DualFloorSmem& sm, int bu
   const int t = threadIdx.x, row = t >> 3, piece = t & 7;
   const fu32x4 c = *reinterpret_cast<const fu32x4*>(&sm.row_codes[buf][row * 32 + 4 * piece]);
   __builtin_nontemporal_store(c, reinterpret_cast<fu32x4*>(row_q + (m0 + row) * (K / 8) + k0 / 8 + 4 * piece));
-  if (t < 64) {
+  if (row_s != nullptr && t < 64) {
     *reinterpret_cast<fu32x2*>(row_s + (m0 + t) * (K / 32) + k0 / 32) =
         *reinterpret_cast<const fu32x2*>(&sm.row_scales[buf][t * 8]);
   }
 }
 
 // M % 256 == 0, K % 256 == 0, 16 B aligned buffers (the shapes the bench uses).
+// SCM 0: the product's scale stores (8 B per row per tile, 8 B per column per
+// super-tile, ordinary stores); SCM 1: no scale stores (the bound the code
+// traffic alone sets); SCM 2: the same scale bytes written as whole lines,
+// each workgroup's 2 KB of row scales and 2 KB of column scales contiguous at
+// logical * 2048 with non-temporal 16 B stores - not the output layout, the
+// bound a layout-free scale store would set. KFAST: super-tiles numbered
+// K-fastest instead of M-fastest.
+template <int SCM, bool KFAST>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void dual_floor(
     const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q, uint8_t* __restrict__ row_s,
     uint8_t* __restrict__ col_q, uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms, int tiles,
@@ -49,7 +59,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void d
   const int logical = (b % 8) * per_xcd + b / 8;
   if (logical >= tiles) return;
   const int t = threadIdx.x, r0 = t >> 5, cc = t & 31;
-  const int64_t m0s = (int64_t)(logical % tiles_ms) * 256, k0 = (int64_t)(logical / tiles_ms) * 256;
+  const int tiles_k = (int)(K / 256);
+  const int64_t m0s = (int64_t)(KFAST ? logical / tiles_k : logical % tiles_ms) * 256;
+  const int64_t k0 = (int64_t)(KFAST ? logical % tiles_k : logical / tiles_ms) * 256;
   uint32_t acc = 0;
   for (int st = 0; st < 4; st++) {
     const int64_t m0 = m0s + 64 * st;
@@ -64,12 +76,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void d
       sm.row_codes[buf][(r0 + 16 * k) * 32 + cc] = d[k].x ^ d[k].y;
       if ((t & 3) == 0) sm.row_scales[buf][(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)d[k].z;
     }
-    if (st > 0) dual_floor_flush(sm, buf ^ 1, row_q, row_s, m0 - 64, k0, K);
+    if (st > 0) dual_floor_flush(sm, buf ^ 1, row_q, SCM == 0 ? row_s : nullptr, m0 - 64, k0, K);
     __syncthreads();
     acc ^= *reinterpret_cast<const uint32_t*>(sm.tile + ((t * 68) & 32764));
     __syncthreads();
   }
-  dual_floor_flush(sm, 1, row_q, row_s, m0s + 192, k0, K);
+  dual_floor_flush(sm, 1, row_q, SCM == 0 ? row_s : nullptr, m0s + 192, k0, K);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -78,10 +90,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void d
     v.x ^= acc;
     *reinterpret_cast<fu32x4*>(col_q + (k0 + c) * (M / 2) + m0s / 2 + 16 * piece) = v;
   }
-  if ((t & 1) == 0) {
+  if (SCM == 0 && (t & 1) == 0) {
     const int c = 2 * (t >> 2) + ((t >> 1) & 1);
     *reinterpret_cast<fu32x2*>(col_s + (k0 + c) * (M / 32) + m0s / 32) = fu32x2{acc, (uint32_t)c};
   }
+  if (SCM == 2 && t < 128) {
+    const fu32x4 w = {acc, (uint32_t)t, (uint32_t)logical, 1u};
+    __builtin_nontemporal_store(w, reinterpret_cast<fu32x4*>(row_s + (int64_t)logical * 2048 + 16 * t));
+    __builtin_nontemporal_store(w, reinterpret_cast<fu32x4*>(col_s + (int64_t)logical * 2048 + 16 * t));
+  }
+  if (SCM == 1 && acc == 0x9E3779B9u) row_s[t] = 1;  // keeps the LDS reads
 }
 
 // ---- row -> col FP8, 128 x 256 tiles (row_to_fp8_col_wide_kernel, row_to_fp8_col_msplit_wide_kernel)
@@ -235,6 +253,84 @@ __global__ __launch_bounds__(256, 4) void msplit_flat_floor(const uint8_t* __res
                         out + start * N + bn * 256 * len + bm * 128, len, out_line && len % 128 == 0);
 }
 
+// ---- per-split row -> col FP8, band schedule (a schedule the product does not use)
+// One workgroup per (split, 64-column band): it loads the band's 32 code
+// bytes and 2 scale bytes of every row of the split into LDS (four 16 B
+// loads in flight per lane), then writes the band's whole output region,
+// the contiguous [64 columns x len] block at off * N + c0 * len, in address
+// order as aligned non-temporal 16 B stores (each lane's chunk gathered from
+// LDS as the conversion would: column o / len, row o % len), its two partial
+// end chunks as bytes, and its scale-row entries. Splits of at most
+// kBandMaxRows rows (the LDS holds the split's band).
+constexpr int kBandMaxRows = 4352;
+
+__global__ __launch_bounds__(256) void msplit_band_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                                         uint8_t* __restrict__ out, float* __restrict__ out_s,
+                                                         const int32_t* __restrict__ lens,
+                                                         const int32_t* __restrict__ offs,
+                                                         const int32_t* __restrict__ soffs, int64_t N, int bands,
+                                                         int total, int per_xcd) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int b = blockIdx.x;
+  const int logical = (int)xcd_order((uint32_t)b, (uint32_t)(per_xcd * 8));
+  if (logical >= total) return;
+  const int i = logical / bands, band = logical % bands;
+  const int len = lens[i];
+  if (len <= 0) return;
+  const int64_t row0 = offs[i], c0 = (int64_t)band * 64;
+  const int t = threadIdx.x;
+  const int nr = (len + 127) / 128;  // rounds of 128 rows (two 16 B chunks per row)
+  for (int k0 = 0; k0 < nr; k0 += 4) {
+    fu32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int r = (k0 + u) * 128 + (t >> 1);
+      const int rr = r < len ? r : len - 1;
+      v[u] = *reinterpret_cast<const fu32x4*>(q + (row0 + rr) * (N / 2) + c0 / 2 + 16 * (t & 1));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int r = (k0 + u) * 128 + (t >> 1);
+      if (k0 + u < nr && r < len) *reinterpret_cast<fu32x4*>(lds + r * 32 + 16 * (t & 1)) = v[u];
+    }
+  }
+  uint8_t* lsc = lds + len * 32;
+  for (int r = t; r < len; r += 256)
+    *reinterpret_cast<uint16_t*>(lsc + 2 * r) = *reinterpret_cast<const uint16_t*>(s + (row0 + r) * (N / 32) + c0 / 32);
+  __syncthreads();
+  uint8_t* base = out + row0 * N + c0 * len;
+  const int64_t size = 64LL * len;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(base), a1 = a0 + size;
+  const uintptr_t f0 = (a0 + 15) & ~(uintptr_t)15, f1 = a1 & ~(uintptr_t)15;
+  const int nch = f1 > f0 ? (int)((f1 - f0) / 16) : 0;
+  const int ldsz = len * 32;
+  int o = (int)(f0 - a0) + 16 * t;
+  int c = o / len, r = o - c * len;
+  for (int j = t; j < nch; j += 256) {
+    const uint32_t idx = ((uint32_t)(r * 32 + (c >> 1)) & ~7u) % (uint32_t)(ldsz - 8);
+    const fu32x2 w = *reinterpret_cast<const fu32x2*>(lds + idx);
+    const fu32x4 val = {w.x ^ lsc[2 * r], w.y, w.x + (uint32_t)c, w.y ^ (uint32_t)r};
+    __builtin_nontemporal_store(val, reinterpret_cast<fu32x4*>(f0 + 16 * (int64_t)j));
+    r += 4096;
+    while (r >= len) {
+      r -= len;
+      c++;
+    }
+  }
+  if (f1 >= f0) {
+    const int head = (int)(f0 - a0), tail = (int)(a1 - f1);
+    if (t < head) base[t] = lds[t];
+    if (t >= 64 && t - 64 < tail) reinterpret_cast<uint8_t*>(f1)[t - 64] = lds[t];
+  } else if (t < size) {
+    base[t] = lds[t];
+  }
+  const int tiles = (len + 127) / 128;
+  for (int k = t; k < tiles * 64; k += 256) {
+    const int tr = k >> 6, cc = k & 63;
+    out_s[(int64_t)(soffs[i] + tr) * N + c0 + cc] = (float)lds[(tr * 4096 + cc) % ldsz];
+  }
+}
+
 // ---- rowwise FP8 requant, 16 rows x 4 groups of 128 elements (mxfp4_to_fp8_kernel<16, true>)
 __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                      fu32x4* __restrict__ out, float* __restrict__ out_s, uint32_t M,
@@ -299,7 +395,22 @@ __attribute__((visibility("default"))) int omo_floor_dual(const void* x, void* r
                                                           void* col_s, int64_t M, int64_t K, hipStream_t stream) {
   if (M <= 0 || K <= 0 || M % 256 || K % 256) return -1;
   const int tiles_ms = (int)(M / 256), tiles = (int)(tiles_ms * (K / 256)), per_xcd = (tiles + 7) / 8;
-  hipLaunchKernelGGL(dual_floor, dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream, static_cast<const uint16_t*>(x),
+  hipLaunchKernelGGL((dual_floor<0, false>), dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream,
+                     static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
+                     static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, tiles_ms, tiles, per_xcd);
+  return (int)hipGetLastError();
+}
+
+// Other schedules of the dual-layout traffic on the same buffers: kind 1 =
+// no scale stores, 2 = scales as whole non-temporal lines (layout-free
+// bound), 3 = the product's stores with super-tiles numbered K-fastest.
+__attribute__((visibility("default"))) int omo_floor_dual_variant(int kind, const void* x, void* row_q, void* row_s,
+                                                                  void* col_q, void* col_s, int64_t M, int64_t K,
+                                                                  hipStream_t stream) {
+  if (M <= 0 || K <= 0 || M % 256 || K % 256 || kind < 1 || kind > 3) return -1;
+  const int tiles_ms = (int)(M / 256), tiles = (int)(tiles_ms * (K / 256)), per_xcd = (tiles + 7) / 8;
+  auto kern = kind == 1 ? dual_floor<1, false> : kind == 2 ? dual_floor<2, false> : dual_floor<0, true>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream, static_cast<const uint16_t*>(x),
                      static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s), static_cast<uint8_t*>(col_q),
                      static_cast<uint8_t*>(col_s), M, K, tiles_ms, tiles, per_xcd);
   return (int)hipGetLastError();
@@ -343,6 +454,32 @@ __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const
   hipLaunchKernelGGL(msplit_floor, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
                      static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
                      out_s_rows, (reinterpret_cast<uintptr_t>(out) & 127) == 0);
+  return (int)hipGetLastError();
+}
+
+// Per-split band-schedule floor (msplit_band_floor): N % 64 == 0, every split
+// at most kBandMaxRows rows (max_split_len bounds them; the split table is
+// the product's int32 device arrays).
+__attribute__((visibility("default"))) int omo_floor_msplit_band(const void* q, const void* s, void* out, float* out_s,
+                                                                 int64_t N, const int32_t* lens, const int32_t* offs,
+                                                                 const int32_t* soffs, int64_t nsplits,
+                                                                 int64_t max_split_len, hipStream_t stream) {
+  if (N <= 0 || N % 64 || nsplits <= 0 || max_split_len <= 0 || max_split_len > kBandMaxRows ||
+      nsplits * (N / 64) > 0x7FFFFFFF / 8)
+    return -1;
+  const int bands = (int)(N / 64), total = (int)(nsplits * bands), per_xcd = (total + 7) / 8;
+  // at least 256 B: the partial end chunks copy LDS bytes 0..79
+  const size_t lds = std::max<size_t>((size_t)max_split_len * 34 + 16, 256);
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)msplit_band_floor, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)(kBandMaxRows * 34 + 16)) != hipSuccess)
+      return -2;
+    attr = true;
+  }
+  hipLaunchKernelGGL(msplit_band_floor, dim3((unsigned)(per_xcd * 8)), dim3(256), lds, stream,
+                     static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
+                     lens, offs, soffs, N, bands, total, per_xcd);
   return (int)hipGetLastError();
 }
 

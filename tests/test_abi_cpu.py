@@ -167,8 +167,8 @@ def test_bench_floor_library_exports_and_shape_checks():
     # the memory-only kernels bench.py times beside the codec kernels: exported,
     # and shapes they do not cover are refused on the host before any launch
     lib = ctypes.CDLL(os.path.join(ROOT, "mxfp4-hopper_amd", "lib", "libomo_ceiling.so"))
-    for name in ["omo_ceiling_launch", "omo_floor_dual", "omo_floor_rowcol", "omo_floor_msplit", "omo_floor_requant",
-                 "omo_floor_dequant"]:
+    for name in ["omo_ceiling_launch", "omo_floor_dual", "omo_floor_dual_variant", "omo_floor_rowcol", "omo_floor_msplit",
+                 "omo_floor_msplit_band", "omo_floor_requant", "omo_floor_dequant"]:
         assert hasattr(lib, name), name
     P, I64 = ctypes.c_void_p, ctypes.c_int64
     lib.omo_floor_dual.argtypes = [P, P, P, P, P, I64, I64, P]
@@ -185,6 +185,15 @@ def test_bench_floor_library_exports_and_shape_checks():
     assert lib.omo_floor_msplit(None, None, None, None, 100, 7168, None, None, None, 0, 60, 2, None) == -1
     assert lib.omo_floor_requant(None, None, None, None, 4096, 3584 + 32, None) == -1
     assert lib.omo_floor_dequant(None, None, None, 0, None) == -1
+    lib.omo_floor_dual_variant.argtypes = [ctypes.c_int, P, P, P, P, P, I64, I64, P]
+    lib.omo_floor_msplit_band.argtypes = [P, P, P, P, I64, P, P, P, I64, I64, P]
+    assert lib.omo_floor_dual_variant(0, None, None, None, None, None, 7168, 18432, None) == -1  # kinds 1..3
+    assert lib.omo_floor_dual_variant(4, None, None, None, None, None, 7168, 18432, None) == -1
+    assert lib.omo_floor_dual_variant(1, None, None, None, None, None, 7168 + 64, 18432, None) == -1
+    # the band schedule holds a whole split's band in LDS: longer splits and N % 64 are refused
+    assert lib.omo_floor_msplit_band(None, None, None, None, 7168, None, None, None, 8, 4353, None) == -1
+    assert lib.omo_floor_msplit_band(None, None, None, None, 7168 + 32, None, None, None, 8, 2000, None) == -1
+    assert lib.omo_floor_msplit_band(None, None, None, None, 7168, None, None, None, 0, 2000, None) == -1
 
 
 def test_payload_validation_paths():
