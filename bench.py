@@ -271,7 +271,11 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
                              (2, "dual_scales_as_whole_lines", "the product's schedule with each workgroup's 4 KB of "
                                                                "scale bytes stored as whole non-temporal lines "
                                                                "(layout-free bound; not a valid output)"),
-                             (3, "dual_k_fastest", "the product's stores with super-tiles numbered K-fastest")):
+                             (3, "dual_k_fastest", "the product's stores in contiguous K-fastest super-tile "
+                                                   "ranges per XCD"),
+                             (4, "dual_m_fastest_ranges", "the product's stores in contiguous M-fastest super-tile "
+                                                          "ranges per XCD (each XCD finishing a band before the "
+                                                          "next)")):
         alt(name, f"dual-layout floor 7168x18432: {what}", wl.dual_quant_bytes(n), 2,
             lambda i, kind=kind: chk(fl.omo_floor_dual_variant(kind, xd[i].data_ptr(), od[i][0].data_ptr(),
                                                                od[i][1].data_ptr(), od[i][2].data_ptr(),

@@ -41,27 +41,59 @@ __device__ __forceinline__ void dual_floor_flush(const DualFloorSmem& sm, int bu
   }
 }
 
+// The product's band-group order (quant_dual_super_kernel): super-tiles
+// numbered M-fastest (L = band * S + super-row) are cut into eight
+// contiguous ranges of per_xcd, one per XCD, and each XCD walks its range
+// super-row by super-row. False past the XCD's range.
+__device__ __forceinline__ bool floor_band_group(int xcd, int j, int S, int T, int per_xcd, int* ms, int* kb) {
+  const int lo = xcd * per_xcd, hi = min(T, lo + per_xcd);
+  if (j >= hi - lo) return false;
+  const int kb0 = lo / S, ms0 = lo - kb0 * S, kb1 = hi / S, ms1 = hi - kb1 * S;
+  auto below = [&](int m) {  // tiles of the range in super-rows below m
+    if (kb0 == kb1) return max(0, min(m, ms1) - ms0);
+    return m * (kb1 - kb0 - 1) + max(0, m - ms0) + min(m, ms1);
+  };
+  int a = 0, b = S;
+  while (b - a > 1) {
+    const int mid = (a + b) >> 1;
+    if (below(mid) <= j) a = mid;
+    else b = mid;
+  }
+  *ms = a;
+  *kb = kb0 + (a >= ms0 ? 0 : 1) + (j - below(a));
+  return true;
+}
+
 // M % 256 == 0, K % 256 == 0, 16 B aligned buffers (the shapes the bench uses).
 // SCM 0: the product's scale stores (8 B per row per tile, 8 B per column per
 // super-tile, ordinary stores); SCM 1: no scale stores (the bound the code
 // traffic alone sets); SCM 2: the same scale bytes written as whole lines,
 // each workgroup's 2 KB of row scales and 2 KB of column scales contiguous at
-// logical * 2048 with non-temporal 16 B stores - not the output layout, the
-// bound a layout-free scale store would set. KFAST: super-tiles numbered
-// K-fastest instead of M-fastest.
-template <int SCM, bool KFAST>
+// its tile number * 2048 with non-temporal 16 B stores - not the output
+// layout, the bound a layout-free scale store would set. ORDER 0: the
+// product's band-group order; 1: contiguous ranges of the M-fastest
+// numbering per XCD (each XCD finishing one band before the next); 2:
+// contiguous ranges of the K-fastest numbering.
+template <int SCM, int ORDER>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void dual_floor(
     const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q, uint8_t* __restrict__ row_s,
     uint8_t* __restrict__ col_q, uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms, int tiles,
     int per_xcd) {
   __shared__ DualFloorSmem sm;
   const int b = blockIdx.x;
-  const int logical = (b % 8) * per_xcd + b / 8;
-  if (logical >= tiles) return;
   const int t = threadIdx.x, r0 = t >> 5, cc = t & 31;
   const int tiles_k = (int)(K / 256);
-  const int64_t m0s = (int64_t)(KFAST ? logical / tiles_k : logical % tiles_ms) * 256;
-  const int64_t k0 = (int64_t)(KFAST ? logical % tiles_k : logical / tiles_ms) * 256;
+  int ms, kb, logical;
+  if (ORDER == 0) {
+    if (!floor_band_group(b % 8, b / 8, tiles_ms, tiles, per_xcd, &ms, &kb)) return;
+    logical = kb * tiles_ms + ms;
+  } else {
+    logical = (b % 8) * per_xcd + b / 8;
+    if (logical >= tiles) return;
+    ms = ORDER == 2 ? logical / tiles_k : logical % tiles_ms;
+    kb = ORDER == 2 ? logical % tiles_k : logical / tiles_ms;
+  }
+  const int64_t m0s = (int64_t)ms * 256, k0 = (int64_t)kb * 256;
   uint32_t acc = 0;
   for (int st = 0; st < 4; st++) {
     const int64_t m0 = m0s + 64 * st;
@@ -233,17 +265,21 @@ __global__ __launch_bounds__(256, 4) void msplit_flat_floor(const uint8_t* __res
     start_l = offs[lane];
     sstart_l = soffs[lane];
   }
-  const int tiles_l = len_l > 0 ? (int)min(((int64_t)len_l + 127) / 128, (int64_t)tm) : 0;
-  const int incl = wave_prefix(tiles_l), excl = incl - tiles_l;
-  const uint32_t n_real = (uint32_t)__builtin_amdgcn_readlane(incl, 63) * (uint32_t)bands;
-  if (blockIdx.x >= n_real) return;
-  const uint32_t L = xcd_order(blockIdx.x, n_real);
-  const uint64_t hit =
-      __ballot(tiles_l > 0 && L >= (uint32_t)bands * (uint32_t)excl && L < (uint32_t)bands * (uint32_t)incl);
+  // the product's band walk: split after split, each XCD takes a contiguous
+  // range of ceil(tiles_i / 8) of the split's band-major tiles and walks it
+  // row tile by row tile
+  const int xcd = (int)(blockIdx.x & 7u), j = (int)(blockIdx.x >> 3);
+  const int rows_l = len_l > 0 ? (int)min(((int64_t)len_l + 127) / 128, (int64_t)tm) : 0;
+  const int per_l = (rows_l * bands + 7) / 8;
+  const int n_l = min(max(rows_l * bands - xcd * per_l, 0), per_l);
+  const int incl = wave_prefix(n_l), excl = incl - n_l;
+  if (j >= __builtin_amdgcn_readlane(incl, 63)) return;
+  const uint64_t hit = __ballot(j >= excl && j < incl);
   const int i = (int)__builtin_ctzll(hit);
-  const uint32_t ti = (uint32_t)__builtin_amdgcn_readlane(tiles_l, i);
-  const uint32_t r = L - (uint32_t)bands * (uint32_t)__builtin_amdgcn_readlane(excl, i);
-  const int64_t bm = r % ti, bn = r / ti;
+  const int S = __builtin_amdgcn_readlane(rows_l, i), per = __builtin_amdgcn_readlane(per_l, i);
+  int tbm, tbn;
+  if (!floor_band_group(xcd, j - __builtin_amdgcn_readlane(excl, i), S, S * bands, per, &tbm, &tbn)) return;
+  const int64_t bm = tbm, bn = tbn;
   const int64_t len = __builtin_amdgcn_readlane(len_l, i), start = __builtin_amdgcn_readlane(start_l, i),
                 sstart = __builtin_amdgcn_readlane(sstart_l, i);
   if (bm * 128 >= len) return;
@@ -395,7 +431,7 @@ __attribute__((visibility("default"))) int omo_floor_dual(const void* x, void* r
                                                           void* col_s, int64_t M, int64_t K, hipStream_t stream) {
   if (M <= 0 || K <= 0 || M % 256 || K % 256) return -1;
   const int tiles_ms = (int)(M / 256), tiles = (int)(tiles_ms * (K / 256)), per_xcd = (tiles + 7) / 8;
-  hipLaunchKernelGGL((dual_floor<0, false>), dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream,
+  hipLaunchKernelGGL((dual_floor<0, 0>), dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream,
                      static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
                      static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, tiles_ms, tiles, per_xcd);
   return (int)hipGetLastError();
@@ -403,13 +439,14 @@ __attribute__((visibility("default"))) int omo_floor_dual(const void* x, void* r
 
 // Other schedules of the dual-layout traffic on the same buffers: kind 1 =
 // no scale stores, 2 = scales as whole non-temporal lines (layout-free
-// bound), 3 = the product's stores with super-tiles numbered K-fastest.
+// bound), 3 = the product's stores in contiguous K-fastest ranges per XCD,
+// 4 = in contiguous M-fastest ranges per XCD.
 __attribute__((visibility("default"))) int omo_floor_dual_variant(int kind, const void* x, void* row_q, void* row_s,
                                                                   void* col_q, void* col_s, int64_t M, int64_t K,
                                                                   hipStream_t stream) {
-  if (M <= 0 || K <= 0 || M % 256 || K % 256 || kind < 1 || kind > 3) return -1;
+  if (M <= 0 || K <= 0 || M % 256 || K % 256 || kind < 1 || kind > 4) return -1;
   const int tiles_ms = (int)(M / 256), tiles = (int)(tiles_ms * (K / 256)), per_xcd = (tiles + 7) / 8;
-  auto kern = kind == 1 ? dual_floor<1, false> : kind == 2 ? dual_floor<2, false> : dual_floor<0, true>;
+  auto kern = kind == 1 ? dual_floor<1, 0> : kind == 2 ? dual_floor<2, 0> : kind == 3 ? dual_floor<0, 2> : dual_floor<0, 1>;
   hipLaunchKernelGGL(kern, dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream, static_cast<const uint16_t*>(x),
                      static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s), static_cast<uint8_t*>(col_q),
                      static_cast<uint8_t*>(col_s), M, K, tiles_ms, tiles, per_xcd);
@@ -443,8 +480,9 @@ __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const
   const int per_wg = device_lds() / 4 - 2560;
   const size_t reserve = per_wg > kWideSmemBytes ? (size_t)(per_wg - kWideSmemBytes) : 0;
   const int64_t tm = (max_split_len + 127) / 128, bands = N / 256;
-  if (nsplits <= 64 && tm * bands <= (int64_t)UINT32_MAX / 256 / nsplits) {
-    hipLaunchKernelGGL(msplit_flat_floor, dim3((unsigned)(nsplits * tm * bands)), dim3(256), reserve, stream,
+  if (nsplits <= 64 && tm * bands + 7 <= (int64_t)UINT32_MAX / 256 / nsplits) {
+    hipLaunchKernelGGL(msplit_flat_floor, dim3((unsigned)(8 * nsplits * ((tm * bands + 7) / 8))), dim3(256), reserve,
+                       stream,
                        static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
                        lens, offs, soffs, total_rows, N, out_s_rows, (reinterpret_cast<uintptr_t>(out) & 127) == 0,
                        (int)nsplits, (int)tm, (int)bands);

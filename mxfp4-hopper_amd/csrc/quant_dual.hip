@@ -248,10 +248,10 @@ __device__ __forceinline__ void dual_row_flush(const DualSuperSmem& sm, int buf,
 
 __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
                                             uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
-                                            uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms,
-                                            int logical, float eps, int c_eps, DualSuperSmem& sm) {
+                                            uint8_t* __restrict__ col_s, int64_t M, int64_t K, int ms, int kb,
+                                            float eps, int c_eps, DualSuperSmem& sm) {
   const int t = threadIdx.x;
-  const int64_t m0s = (int64_t)(logical % tiles_ms) * kSuperRows, k0 = (int64_t)(logical / tiles_ms) * kDualCols;
+  const int64_t m0s = (int64_t)ms * kSuperRows, k0 = (int64_t)kb * kDualCols;
   const int steps = (int)((M - m0s) / kDualRows < kSuperSteps ? (M - m0s) / kDualRows : kSuperSteps);
   const int r0 = t >> 5, cc = t & 31;
   const bool quad_leader = (t & 3) == 0;
@@ -353,6 +353,44 @@ __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint
   }
 }
 
+// Super-tile order of the four-tile kernels. The S x B super-tiles of a
+// tensor (S super-rows, B bands of 256 columns), numbered M-fastest
+// (L = band * S + super-row), are cut into eight contiguous ranges of
+// per_xcd = ceil(S * B / 8), one per XCD, so each XCD owns a group of whole
+// bands (the ends of its range may be parts of bands). Each XCD walks its
+// range super-row by super-row: all of its bands of super-row m, then those of
+// m + 1. The eight XCDs thus sweep the tensor's rows together: at any moment
+// the chip reads a few whole 256-row stripes of the input, each row's codes
+// are written by all XCDs at about the same time, and each XCD's column codes
+// fill its own contiguous region. Memory-only copies of the schedule at 7168 x
+// 18432 (heavy-tailed weights, rotating buffers): 68.0 us against 73.3 us for
+// M-fastest ranges (each XCD finishing one band before the next) and 73.4 us
+// for K-fastest ones (the XCDs on different stripes), which also write 10 MB
+// more (scale lines leaving L2 partly filled); the kernel 71.6 us against
+// 76.6 us in M-fastest ranges. Returns false past the XCD's range.
+__device__ __forceinline__ bool band_group_tile(int xcd, int j, int S, int T, int per_xcd, int* ms, int* kb) {
+  const int lo = xcd * per_xcd, hi = min(T, lo + per_xcd);
+  if (j >= hi - lo) return false;
+  const int kb0 = lo / S, ms0 = lo - kb0 * S;  // first tile of the range
+  const int kb1 = hi / S, ms1 = hi - kb1 * S;  // one past the last
+  // tiles of the range in super-rows below m: band kb0 holds super-rows
+  // [ms0, S) (or [ms0, ms1) when kb0 == kb1), bands kb0 + 1 .. kb1 - 1 all,
+  // band kb1 [0, ms1)
+  auto below = [&](int m) {
+    if (kb0 == kb1) return max(0, min(m, ms1) - ms0);
+    return m * (kb1 - kb0 - 1) + max(0, m - ms0) + min(m, ms1);
+  };
+  int a = 0, b = S;  // below(a) <= j < below(b) = hi - lo
+  while (b - a > 1) {
+    const int mid = (a + b) >> 1;
+    if (below(mid) <= j) a = mid;
+    else b = mid;
+  }
+  *ms = a;
+  *kb = kb0 + (a >= ms0 ? 0 : 1) + (j - below(a));
+  return true;
+}
+
 // At most 80 VGPRs (six waves per SIMD): three 512-thread workgroups per CU,
 // which the LDS (52 KB each) also allows; at 86 the compiler's own choice,
 // two fit and the kernel ran 8% slower.
@@ -362,27 +400,40 @@ __global__ __launch_bounds__(kDualThreads) __attribute__((amdgpu_waves_per_eu(6)
     int per_xcd, float eps, int c_eps) {
   __shared__ DualSuperSmem sm;
   const int b = blockIdx.x;
-  const int logical = (b % kXcds) * per_xcd + b / kXcds;
-  if (logical >= tiles) return;
-  dual_super4(x, row_q, row_s, col_q, col_s, M, K, tiles_ms, logical, eps, c_eps, sm);
+  int ms, kb;
+  if (!band_group_tile(b % kXcds, b / kXcds, tiles_ms, tiles, per_xcd, &ms, &kb)) return;
+  dual_super4(x, row_q, row_s, col_q, col_s, M, K, ms, kb, eps, c_eps, sm);
 }
 
+// band_group: the 64-row tiles in band-group order (band_group_tile over
+// tiles instead of super-tiles), else each XCD takes a contiguous M-fastest
+// range. Measured (graph replays): 8192 x 7168 37.1 us against 38.3, 4096 x
+// 7168 20.7 against 21.1; with fewer than six tiles per CU the ranges are
+// ahead (7168 x 2048 11.7 against 12.0, 2048 x 2048 5.5 against 5.9).
 __global__ __launch_bounds__(kDualThreads) void quant_dual_kernel(const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q,
                                                          uint8_t* __restrict__ row_s, uint8_t* __restrict__ col_q,
                                                          uint8_t* __restrict__ col_s, int64_t M, int64_t K,
-                                                         int tiles_m, int tiles, int per_xcd, float eps, int c_eps) {
+                                                         int tiles_m, int tiles, int per_xcd, bool band_group, float eps,
+                                                         int c_eps) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
   __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
   const int b = blockIdx.x;
-  const int logical = (b % kXcds) * per_xcd + b / kXcds;
-  if (logical >= tiles) return;
+  int logical;
+  if (band_group) {
+    int ms, kb;
+    if (!band_group_tile(b % kXcds, b / kXcds, tiles_m, tiles, per_xcd, &ms, &kb)) return;
+    logical = kb * tiles_m + ms;
+  } else {
+    logical = (b % kXcds) * per_xcd + b / kXcds;
+    if (logical >= tiles) return;
+  }
   dual_tile(x, row_q, row_s, col_q, col_s, M, K, tiles_m, logical, eps, c_eps, tile, rs_tile);
 }
 
 // Grouped form: one launch over up to kDualGroupMax tensors (e.g. the weights
-// of all local experts), whose tiles are numbered item after item and then
-// spread over the XCDs like the tiles of one tensor. The descriptor table
-// travels by value in the kernel arguments.
+// of all local experts). Every XCD takes its band-group share of each item,
+// item after item, so the XCDs sweep the items one after another together.
+// The descriptor table travels by value in the kernel arguments.
 struct DualItem {
   const uint16_t* x;
   uint32_t* row_q;
@@ -390,7 +441,8 @@ struct DualItem {
   uint8_t* col_q;
   uint8_t* col_s;
   int64_t M, K;
-  int tiles_m, tile_begin;  // first logical tile of this item
+  int tiles_m;         // the item's tile rows (64 or 256 rows each, by kernel)
+  int tiles, per_xcd;  // its tiles and their per-XCD share
 };
 
 struct DualGroup {
@@ -399,32 +451,48 @@ struct DualGroup {
   float eps;
 };
 
+// Each XCD takes its band-group share of each item, item after item, over
+// the items' 64-row tiles. cfg5's 24 expert weights (three shapes of 7168 x
+// 2048 / 2048 x 7168, 224 super-tiles each): 208.8 us against 212.3 us for
+// the four-tile kernel over contiguous ranges of all items' super-tiles; on
+// zero-filled buffers 203.7 us against 224.4 us with contiguous ranges of the
+// 64-row tiles and 211.6 us for the four-tile kernel in band groups.
 __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const DualGroup g) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
   __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
-  const int b = blockIdx.x;
-  const int logical = (b % kXcds) * g.per_xcd + b / kXcds;
-  if (logical >= g.tiles) return;
-  int i = 0;
-  while (i + 1 < g.count && logical >= g.item[i + 1].tile_begin) i++;
+  const int b = blockIdx.x, xcd = b % kXcds;
+  int j = b / kXcds, i = 0;
+  for (; i < g.count; i++) {
+    const int n = min(max(g.item[i].tiles - xcd * g.item[i].per_xcd, 0), g.item[i].per_xcd);
+    if (j < n) break;
+    j -= n;
+  }
+  if (i == g.count) return;
   const DualItem& it = g.item[i];
-  dual_tile(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, it.tiles_m, logical - it.tile_begin, g.eps,
-            g.c_eps, tile, rs_tile);
+  int ms, kb;
+  if (!band_group_tile(xcd, j, it.tiles_m, it.tiles, it.per_xcd, &ms, &kb)) return;
+  dual_tile(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, it.tiles_m, kb * it.tiles_m + ms, g.eps, g.c_eps,
+            tile, rs_tile);
 }
 
 // Grouped form of quant_dual_super_kernel: every item has M % 64 == 0,
-// K % 256 == 0 and aligned buffers; tiles_m and tile_begin count super-tiles.
+// K % 256 == 0 and aligned buffers; tiles_m counts super-rows.
 __global__ __launch_bounds__(kDualThreads) __attribute__((amdgpu_waves_per_eu(6))) void quant_dual_grouped_super_kernel(
     const DualGroup g) {
   __shared__ DualSuperSmem sm;
-  const int b = blockIdx.x;
-  const int logical = (b % kXcds) * g.per_xcd + b / kXcds;
-  if (logical >= g.tiles) return;
-  int i = 0;
-  while (i + 1 < g.count && logical >= g.item[i + 1].tile_begin) i++;
+  const int b = blockIdx.x, xcd = b % kXcds;
+  // the XCD's share of each item, item after item
+  int j = b / kXcds, i = 0;
+  for (; i < g.count; i++) {
+    const int n = min(max(g.item[i].tiles - xcd * g.item[i].per_xcd, 0), g.item[i].per_xcd);
+    if (j < n) break;
+    j -= n;
+  }
+  if (i == g.count) return;
   const DualItem& it = g.item[i];
-  dual_super4(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, it.tiles_m, logical - it.tile_begin, g.eps,
-              g.c_eps, sm);
+  int ms, kb;
+  if (!band_group_tile(xcd, j, it.tiles_m, it.tiles, it.per_xcd, &ms, &kb)) return;
+  dual_super4(it.x, it.row_q, it.row_s, it.col_q, it.col_s, it.M, it.K, ms, kb, g.eps, g.c_eps, sm);
 }
 
 // Shapes and buffers the four-tile kernels take: whole 64 x 256 tiles, 16 B
@@ -453,10 +521,11 @@ hipError_t launch_quant_dual(const void* x, void* row_q, void* row_s, void* col_
                        eps, host_c_eps(eps, 6.0f));
   }
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
+  const bool band_group = tiles >= 6 * (int64_t)current_device_caps().cus;
   return launch(quant_dual_kernel, dim3((unsigned)(per_xcd * kXcds)), dim3(kDualThreads), 0, stream,
                      static_cast<const uint16_t*>(x), static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s),
                      static_cast<uint8_t*>(col_q), static_cast<uint8_t*>(col_s), M, K, (int)tiles_m, (int)tiles,
-                     (int)per_xcd, eps, host_c_eps(eps, 6.0f));
+                     (int)per_xcd, band_group, eps, host_c_eps(eps, 6.0f));
 }
 
 hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps, hipStream_t stream) {
@@ -464,13 +533,16 @@ hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps
     DualGroup g;
     memset(&g, 0, sizeof(g));
     g.count = count - base < kDualGroupMax ? count - base : kDualGroupMax;
+    // the four-tile kernel where every item would take it alone
     bool super = true;
     for (int j = 0; j < g.count; j++) {
       const DualSpec& d = items[base + j];
-      super = super && (d.M == 0 || d.K == 0 || dual_super_ok(d.x, d.row_q, d.col_q, d.M, d.K));
+      const int64_t st = ((d.M + kSuperRows - 1) / kSuperRows) * ((d.K + kDualCols - 1) / kDualCols);
+      super = super && (d.M == 0 || d.K == 0 ||
+                        (dual_super_ok(d.x, d.row_q, d.col_q, d.M, d.K) && st >= 4 * (int64_t)current_device_caps().cus));
     }
     const int unit_rows = super ? kSuperRows : kDualRows;
-    int tiles = 0;
+    int tiles = 0, super_slots = 0;
     for (int j = 0; j < g.count; j++) {
       const DualSpec& d = items[base + j];
       DualItem& it = g.item[j];
@@ -482,12 +554,14 @@ hipError_t launch_quant_dual_grouped(const DualSpec* items, int count, float eps
       it.M = d.M;
       it.K = d.K;
       it.tiles_m = (int)((d.M + unit_rows - 1) / unit_rows);
-      it.tile_begin = tiles;
-      tiles += (d.M == 0 || d.K == 0) ? 0 : it.tiles_m * (int)((d.K + kDualCols - 1) / kDualCols);
+      it.tiles = (d.M == 0 || d.K == 0) ? 0 : it.tiles_m * (int)((d.K + kDualCols - 1) / kDualCols);
+      it.per_xcd = (it.tiles + kXcds - 1) / kXcds;
+      tiles += it.tiles;
+      super_slots += it.per_xcd;  // XCD 0 has the largest share of every item: the grid's slots per XCD
     }
     if (tiles == 0) continue;
     g.tiles = tiles;
-    g.per_xcd = (tiles + kXcds - 1) / kXcds;
+    g.per_xcd = super_slots;
     g.eps = eps;
     g.c_eps = host_c_eps(eps, 6.0f);
     auto kernel = super ? quant_dual_grouped_super_kernel : quant_dual_grouped_kernel;

@@ -806,78 +806,146 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
 // Per split on a flat grid, for at most 128 splits. The tiles that hold rows
 // (ceil(len_i / 128) row tiles of split i, at most the grid's tm, times the
 // column bands) are numbered split by split, band by band, row tile fastest,
-// and spread over the XCDs in contiguous ranges: every XCD gets the same
-// number of real tiles, and the two tiles that share a column's 128 B output
-// lines (row tiles bm and bm + 1) run next to each other on one XCD, where
-// their partial lines merge in L2. Each wave finds its workgroup's tile
-// itself: lane l reads the metadata of splits l + 64k, wave sums give the
-// tile numbering, a ballot the split. Workgroups past the last real tile
-// exit.
+// and handed to the XCDs in one of two orders. Each wave finds its
+// workgroup's tile itself: lane l reads the metadata of splits l + 64k, wave
+// sums number the tiles, a ballot finds the split. Workgroups past the last
+// tile (of their XCD) exit.
+//  * Ranges: the whole numbering is cut into eight contiguous ranges, one per
+//    XCD, so every XCD gets the same number of tiles, and the two row tiles
+//    that share a column's 128 B output lines run next to each other on one
+//    XCD, where their partial lines merge in L2. An XCD then holds about one
+//    split when there are eight.
+//  * Band walk: split after split, the split's tiles are cut into eight
+//    contiguous ranges of ceil(tiles_i / 8), one per XCD, so that each XCD
+//    owns a group of bands (parts of bands at its range's ends), and each XCD
+//    walks its range row tile by row tile (all its bands of row tile m, then
+//    those of m + 1). The XCDs read each split's rows in a shared sweep, and
+//    the row tiles sharing an output line still run a few workgroups apart
+//    on the XCD that owns the column.
+// On 16431 routed rows x 7168 (wide tiles), band walk against ranges: 49.5
+// against 55.4 us for 8 splits (1801..2279 rows), 49.5/54.9 for 4 uneven,
+// 51.0/53.9 for 16, 51.2/52.7 for 32; past 64 splits the ranges win (53.9
+// against 54.3 us at 65, 56.1/57.3 at 100, 60.1/61.7 at 128). The wide
+// kernel walks bands up to 64 splits. With the 128-column tiles (N = 7040)
+// the ranges win at every count (70.0 against 79.4 us at 8 splits, 82.0/91.0
+// at 16) and are always used.
 // On the 3-D grid (split, row tile, band) a split's tiles all land on one
 // XCD when the split count is a multiple of 8 (the XCD holding the longest
 // splits then finishes last) and are scattered otherwise. On 16431 routed
-// rows x 7168 with the same tile code, the flat grid took 52.2-56.1 us for 4
-// to 65 splits of any balance and 57.6 and 62.0 us for 100 and 128 splits;
-// the 3-D grid 54.7 us for cfg5's 8 nearly equal splits, 72-174 us for 4 to
-// 32 uneven ones and 70-74 us for 65 to 128. Past 128 splits the 3-D grid is
+// rows x 7168 with the same tile code, the ranges took 52.2-56.1 us for 4 to
+// 65 splits of any balance and 57.6 and 62.0 us for 100 and 128 splits; the
+// 3-D grid 54.7 us for cfg5's 8 nearly equal splits, 72-174 us for 4 to 32
+// uneven ones and 70-74 us for 65 to 128. Past 128 splits the 3-D grid is
 // kept: hundreds of short splits balance by their number, and four metadata
 // chunks per lane lost there (77.7 against 76.1 us at 200 splits, 82.1
 // against 77.4 at 256).
 constexpr int kFlatMaxSplits = 128;  // lane l of each wave holds splits l and l + 64
 
+// Workgroups of the flat grid, enough for either order: every XCD gets at
+// most ceil(tm * bands / 8) tiles of each split.
+__host__ __device__ constexpr int64_t flat_grid_blocks(int64_t nsplits, int64_t tm, int64_t bands) {
+  return 8 * nsplits * ((tm * bands + 7) / 8);
+}
+
+// Band walk: tile (S row tiles x B bands, T = S * B, numbered band by band
+// with the row tile fastest) of position j in XCD xcd's walk over its
+// contiguous range of per_xcd tiles, row tile by row tile. False past the
+// range.
+__device__ __forceinline__ bool band_walk_tile(int xcd, int j, int S, int T, int per_xcd, int* bm, int* bn) {
+  const int lo = xcd * per_xcd, hi = min(T, lo + per_xcd);
+  if (j >= hi - lo) return false;
+  const int bn0 = lo / S, m0 = lo - bn0 * S;  // first tile of the range
+  const int bn1 = hi / S, m1 = hi - bn1 * S;  // one past the last
+  // tiles of the range in row tiles below m: band bn0 holds [m0, S) (or
+  // [m0, m1) when bn0 == bn1), bands bn0 + 1 .. bn1 - 1 all, band bn1 [0, m1)
+  auto below = [&](int m) {
+    if (bn0 == bn1) return max(0, min(m, m1) - m0);
+    return m * (bn1 - bn0 - 1) + max(0, m - m0) + min(m, m1);
+  };
+  int a = 0, b = S;  // below(a) <= j < below(b) = hi - lo
+  while (b - a > 1) {
+    const int mid = (a + b) >> 1;
+    if (below(mid) <= j) a = mid;
+    else b = mid;
+  }
+  *bm = a;
+  *bn = bn0 + (a >= m0 ? 0 : 1) + (j - below(a));
+  return true;
+}
+
 // The tile of this workgroup on the flat grid: split, row tile bm and band
-// bn, or false past the last real tile (uniform over the workgroup).
-template <int CHUNKS>  // splits per lane: 1 (up to 64 splits) or 2 (up to 128)
+// bn, or false past the last tile (uniform over the workgroup).
+template <int CHUNKS,  // splits per lane: 1 (up to 64 splits) or 2 (up to 128)
+          bool WALK>   // band walk, else ranges
 __device__ __forceinline__ bool flat_split_tile(const int32_t* __restrict__ lens, const int32_t* __restrict__ offs,
                                                 const int32_t* __restrict__ soffs, int nsplits, int tm, int bands,
                                                 int64_t* len, int64_t* start, int64_t* sstart, int64_t* bm,
                                                 int64_t* bn) {
   const int lane = (int)(threadIdx.x & 63);
+  const int xcd = (int)(blockIdx.x & 7u);
   int len_l[CHUNKS], start_l[CHUNKS], sstart_l[CHUNKS];
 #pragma unroll
   for (int k = 0; k < CHUNKS; k++) {
-    const int j = lane + 64 * k;
+    const int i = lane + 64 * k;
     len_l[k] = start_l[k] = sstart_l[k] = 0;
-    if (j < nsplits) {
-      len_l[k] = lens[j];
-      start_l[k] = offs[j];
-      sstart_l[k] = soffs[j];
+    if (i < nsplits) {
+      len_l[k] = lens[i];
+      start_l[k] = offs[i];
+      sstart_l[k] = soffs[i];
     }
   }
-  // tiles of each split, numbered in split order: chunk k's splits follow
-  // the tiles of chunks 0 .. k-1
-  int tiles_l[CHUNKS], lo_l[CHUNKS], hi_l[CHUNKS];
-  uint32_t before = 0;
+  // Each split's share of the numbering, in split order (chunk k's splits
+  // follow those of chunks 0 .. k-1): ranges count whole splits' row tiles
+  // (times bands below), band walk this XCD's tiles of each split.
+  int rows_l[CHUNKS], per_l[CHUNKS], lo_l[CHUNKS], hi_l[CHUNKS];
+  int before = 0;
 #pragma unroll
   for (int k = 0; k < CHUNKS; k++) {
-    tiles_l[k] = len_l[k] > 0 ? (int)min(((int64_t)len_l[k] + kTile - 1) / kTile, (int64_t)tm) : 0;
-    const int incl = wave_inclusive_sum(tiles_l[k]);
-    lo_l[k] = (int)before + incl - tiles_l[k];
-    hi_l[k] = (int)before + incl;
-    before += (uint32_t)__builtin_amdgcn_readlane(incl, 63);
+    rows_l[k] = len_l[k] > 0 ? (int)min(((int64_t)len_l[k] + kTile - 1) / kTile, (int64_t)tm) : 0;
+    per_l[k] = (rows_l[k] * bands + 7) / 8;
+    const int n = WALK ? min(max(rows_l[k] * bands - xcd * per_l[k], 0), per_l[k]) : rows_l[k];
+    const int incl = wave_inclusive_sum(n);
+    lo_l[k] = before + incl - n;
+    hi_l[k] = before + incl;
+    before += __builtin_amdgcn_readlane(incl, 63);
   }
-  // real tiles: at most nsplits * tm * bands, the grid size (below 2^31)
-  const uint32_t n_real = before * (uint32_t)bands;
-  if (blockIdx.x >= n_real) return false;
-  const uint32_t L = xcd_contiguous(blockIdx.x, n_real);
-  // exactly one split's range [bands * lo, bands * hi) holds L
-  uint32_t ti = 1, r = 0;
+  // the position to find: j in this XCD's walk, or L in the whole numbering
+  // (at most nsplits * tm * bands, below the grid size, itself below 2^31)
+  int j;
+  if (WALK) {
+    j = (int)(blockIdx.x >> 3);
+    if (j >= before) return false;
+  } else {
+    const uint32_t n_real = (uint32_t)before * (uint32_t)bands;
+    if (blockIdx.x >= n_real) return false;
+    j = (int)xcd_contiguous(blockIdx.x, n_real);
+  }
+  const int unit = WALK ? 1 : bands;  // numbering units per share unit
+  // exactly one split's range [unit * lo, unit * hi) holds j
+  int S = 1, per = 1, r = 0;
   *len = *start = *sstart = 0;
 #pragma unroll
   for (int k = 0; k < CHUNKS; k++) {
-    const uint64_t hit = __ballot(tiles_l[k] > 0 && L >= (uint32_t)bands * (uint32_t)lo_l[k] &&
-                                  L < (uint32_t)bands * (uint32_t)hi_l[k]);
+    const uint64_t hit = __ballot(j >= unit * lo_l[k] && j < unit * hi_l[k]);
     if (hit) {
       const int i = (int)__builtin_ctzll(hit);
-      ti = (uint32_t)__builtin_amdgcn_readlane(tiles_l[k], i);
-      r = L - (uint32_t)bands * (uint32_t)__builtin_amdgcn_readlane(lo_l[k], i);
+      S = __builtin_amdgcn_readlane(rows_l[k], i);
+      per = __builtin_amdgcn_readlane(per_l[k], i);
+      r = j - unit * __builtin_amdgcn_readlane(lo_l[k], i);
       *len = __builtin_amdgcn_readlane(len_l[k], i);
       *start = __builtin_amdgcn_readlane(start_l[k], i);
       *sstart = __builtin_amdgcn_readlane(sstart_l[k], i);
     }
   }
-  *bm = r % ti;
-  *bn = r / ti;
+  if (WALK) {
+    int tbm, tbn;
+    if (!band_walk_tile(xcd, r, S, S * bands, per, &tbm, &tbn)) return false;
+    *bm = tbm;
+    *bn = tbn;
+  } else {
+    *bm = r % S;
+    *bn = r / S;
+  }
   return true;
 }
 
@@ -888,7 +956,8 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
     int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool out_line, int nsplits, int tm, int bands) {
   __shared__ WideSmem sm;
   int64_t len, start, sstart, bm, bn;
-  if (!flat_split_tile<CHUNKS>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn)) return;
+  if (!flat_split_tile<CHUNKS, CHUNKS == 1>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn))
+    return;
   msplit_wide_tile(sm, q, s, out, out_s, len, start, sstart, bm, bn, total_rows, N, out_s_rows, eps, out_line);
 }
 
@@ -949,7 +1018,7 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_narrow_flat_
     int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool vin, bool vs, int nsplits, int tm, int bands) {
   __shared__ RowColSmem sm;
   int64_t len, start, sstart, bm, bn;
-  if (!flat_split_tile<CHUNKS>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn)) return;
+  if (!flat_split_tile<CHUNKS, false>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn)) return;
   msplit_narrow_tile(sm, q, s, out, out_s, len, start, sstart, bm, bn, total_rows, N, out_s_rows, eps, vin, vs);
 }
 
@@ -998,8 +1067,8 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   // A launch holds at most 2^32 - 1 work-items along x (gridDim.x times the
   // workgroup size), so the flat grid's limit depends on the kernel's width.
   const int64_t flat_threads = wide ? 256 : kRcThreads;
-  if (nsplits <= kFlatMaxSplits && tiles_m * bands <= (int64_t)UINT32_MAX / flat_threads / nsplits) {
-    const dim3 grid((unsigned)(nsplits * tiles_m * bands));
+  if (nsplits <= kFlatMaxSplits && tiles_m * bands + 7 <= (int64_t)UINT32_MAX / flat_threads / nsplits) {
+    const dim3 grid((unsigned)flat_grid_blocks(nsplits, tiles_m, bands));
     if (wide) {
       auto kernel = nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1> : row_to_fp8_col_msplit_flat_kernel<2>;
       return launch(kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
