@@ -232,6 +232,7 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
     fl.omo_floor_dequant.argtypes = [P, P, P, I64, P]
     fl.omo_floor_dual_variant.argtypes = [ctypes.c_int, P, P, P, P, P, I64, I64, P]
     fl.omo_floor_msplit_band.argtypes = [P, P, P, P, I64, P, P, P, I64, I64, P]
+    fl.omo_floor_dual_grouped.argtypes = [ctypes.c_int, P, P, P, P, P, P, P, ctypes.c_int, P]
 
     def chk(rc, what):
         if rc:
@@ -282,6 +283,33 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
                                                                od[i][3].data_ptr(), M, K, cur()), "dual variant"),
             max(20, args.steps // 50), "dual")
     del xd, od
+    # the grouped dual-layout quantize of cfg5's 24 expert weights (one-tile pattern)
+    c5 = wl.CFG5
+    w_shapes = [(c5["hidden"], c5["ffn"]), (c5["hidden"], c5["ffn"]), (c5["ffn"], c5["hidden"])] * c5["local_experts"]
+    nwi = len(w_shapes)
+    bg = sum(wl.dual_quant_bytes(r * c) for r, c in w_shapes)
+    gx = [[wl.normal_bf16(sh, seed=100 + i + 50 * si, device=dev, std=0.02) for i, sh in enumerate(w_shapes)]
+          for si in range(2)]
+    go = [[[torch.empty(b, dtype=torch.uint8, device=dev) for b in (r * c // 2, r * c // 32, r * c // 2, r * c // 32)]
+           for r, c in w_shapes] for _ in range(2)]
+    g_items = [(_abi.DualItem * nwi)(*[_abi.DualItem(w.data_ptr(), w.size(0), w.size(1), *(v for t in o for v in
+                                                                                         (t.data_ptr(), t.numel())))
+                                       for w, o in zip(gx[si], go[si])]) for si in range(2)]
+    PA = ctypes.c_void_p * nwi
+    g_ptrs = [[PA(*[w.data_ptr() for w in gx[si]])] + [PA(*[o[k].data_ptr() for o in go[si]]) for k in range(4)]
+              for si in range(2)]
+    g_m = (ctypes.c_int64 * nwi)(*[r for r, _ in w_shapes])
+    g_k = (ctypes.c_int64 * nwi)(*[c for _, c in w_shapes])
+
+    def g_floor(i, scm):
+        chk(fl.omo_floor_dual_grouped(scm, *g_ptrs[i], g_m, g_k, nwi, cur()), "grouped floor")
+    pair("dual_grouped", "grouped dual-layout quantize of cfg5's 24 expert weights (quant_dual_grouped_kernel)", bg, 2,
+         lambda i: chk(lib.omo_hip_quant_mxfp4_dual_grouped(g_items[i], nwi, 1e-10, cur()), "grouped"),
+         lambda i: g_floor(i, 0), max(10, args.steps // 100))
+    alt("dual_grouped_no_scale_stores", "grouped dual-layout floor without its scale stores (the bound of the code "
+                                        "traffic; not a valid output)", bg, 2, lambda i: g_floor(i, 1),
+        max(10, args.steps // 100), "dual_grouped")
+    del gx, go, g_items, g_ptrs
     # the code-reading kernels at cfg4's 4096 x 7168 (dequant at 8192 x 7168)
     M, N = 4096, 7168
     n = M * N

@@ -134,6 +134,87 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void d
   if (SCM == 1 && acc == 0x9E3779B9u) row_s[t] = 1;  // keeps the LDS reads
 }
 
+// ---- grouped dual-layout quantize, one 64 x 256 tile per workgroup (quant_dual_grouped_kernel)
+constexpr int kFloorGroupMax = 32;
+
+struct FloorItem {
+  const uint16_t* x;
+  uint32_t* row_q;
+  uint8_t* row_s;
+  uint8_t* col_q;
+  uint8_t* col_s;
+  int64_t M, K;
+  int tiles_m, tiles, per_xcd;
+};
+
+struct FloorGroup {
+  FloorItem item[kFloorGroupMax];
+  int count;
+};
+
+// One tile's loads and stores as the product's one-tile kernel issues them
+// (M % 64 == 0, K % 256 == 0): four 16 B non-temporal loads per lane, 4 B
+// non-temporal row-code stores, 64 rows' 8 scale bytes gathered in LDS and
+// stored after the barrier, then per column pair two 8 B code stores and a
+// 2-byte scale store (SCM 1: no scale stores).
+template <int SCM>
+__device__ __forceinline__ void dual_tile_floor(const FloorItem& it, int64_t m0, int64_t k0, uint8_t* tile,
+                                                uint8_t* rs_tile) {
+  const int64_t M = it.M, K = it.K;
+  const int t = threadIdx.x, r0 = t >> 5, cc = t & 31;
+  const int64_t col = k0 + cc * 8;
+  fu32x4 d[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+    d[k] = __builtin_nontemporal_load(reinterpret_cast<const fu32x4*>(it.x + (m0 + r0 + 16 * k) * K + col));
+  uint32_t* rq = it.row_q + (m0 + r0) * (K / 8) + col / 8;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    *reinterpret_cast<fu32x4*>(tile + (r0 + 16 * k) * 512 + ((cc ^ (k << 2)) * 16)) = d[k];
+    __builtin_nontemporal_store(d[k].x ^ d[k].y, rq + k * 2 * K);
+    if ((t & 3) == 0) rs_tile[(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)d[k].z;
+  }
+  __syncthreads();
+  if (SCM == 0 && t < 64)
+    *reinterpret_cast<fu32x2*>(it.row_s + (m0 + t) * (K / 32) + k0 / 32) = *reinterpret_cast<const fu32x2*>(rs_tile + t * 8);
+  const int h = t & 1, g = (t >> 1) & 1, p = t >> 2, band = 2 * g + h;
+  const int64_t kc = k0 + 2 * p;
+  const int pp = 4 * (p ^ (band << 4));
+  uint32_t a0 = 0, a1 = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t w0 = *reinterpret_cast<const uint32_t*>(tile + (16 * band + 2 * j) * 512 + pp);
+    const uint32_t w1 = *reinterpret_cast<const uint32_t*>(tile + (16 * band + 2 * j + 1) * 512 + pp);
+    if (j < 4) a0 ^= w0 ^ (w1 << 1);
+    else a1 ^= w0 ^ (w1 << 1);
+  }
+  const int64_t mo = (m0 + 16 * band) / 2;
+  *reinterpret_cast<fu32x2*>(it.col_q + kc * (M / 2) + mo) = fu32x2{a0, a1};
+  *reinterpret_cast<fu32x2*>(it.col_q + (kc + 1) * (M / 2) + mo) = fu32x2{a1, a0};
+  if (SCM == 0 && h == 0) *reinterpret_cast<uint16_t*>(it.col_s + (kc + g) * (M / 32) + m0 / 32) = (uint16_t)(a0 ^ a1);
+  if (SCM == 1 && a0 == 0x9E3779B9u) it.row_s[t] = 1;  // keeps the LDS reads
+}
+
+// The product's grouped order: each XCD takes its band-group share of each
+// item, item after item.
+template <int SCM>
+__global__ __launch_bounds__(512) void dual_grouped_floor(const FloorGroup g) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[64 * 512];
+  __shared__ __attribute__((aligned(8))) uint8_t rs_tile[64 * 8];
+  const int b = blockIdx.x, xcd = b % 8;
+  int j = b / 8, i = 0;
+  for (; i < g.count; i++) {
+    const int n = min(max(g.item[i].tiles - xcd * g.item[i].per_xcd, 0), g.item[i].per_xcd);
+    if (j < n) break;
+    j -= n;
+  }
+  if (i == g.count) return;
+  const FloorItem& it = g.item[i];
+  int ms, kb;
+  if (!floor_band_group(xcd, j, it.tiles_m, it.tiles, it.per_xcd, &ms, &kb)) return;
+  dual_tile_floor<SCM>(it, (int64_t)ms * 64, (int64_t)kb * 256, tile, rs_tile);
+}
+
 // ---- row -> col FP8, 128 x 256 tiles (row_to_fp8_col_wide_kernel, row_to_fp8_col_msplit_wide_kernel)
 constexpr int kWideSmemBytes = 128 * 160 + 8 * 128 * 4 + 8 * 128;  // the product's WideSmem
 
@@ -539,6 +620,40 @@ __attribute__((visibility("default"))) int omo_floor_dequant(const void* q, cons
   if (ndw <= 0) return -1;
   hipLaunchKernelGGL(dequant_floor, dim3((unsigned)((ndw + 1023) / 1024)), dim3(256), 0, stream,
                      static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<fu32x4*>(out), ndw);
+  return (int)hipGetLastError();
+}
+
+
+// Grouped dual-layout floor over `count` items (at most 32; each M % 64 == 0,
+// K % 256 == 0, 16 B aligned buffers): x[i] [M[i], K[i]] bf16 with the
+// product's four outputs. scm 0 = the product's stores, 1 = no scale stores.
+__attribute__((visibility("default"))) int omo_floor_dual_grouped(int scm, const void* const* x, void* const* row_q,
+                                                                  void* const* row_s, void* const* col_q,
+                                                                  void* const* col_s, const int64_t* M,
+                                                                  const int64_t* K, int count, hipStream_t stream) {
+  if (scm < 0 || scm > 1 || count <= 0 || count > kFloorGroupMax) return -1;
+  FloorGroup g;
+  memset(&g, 0, sizeof(g));
+  g.count = count;
+  int64_t slots = 0;
+  for (int i = 0; i < count; i++) {
+    if (M[i] <= 0 || K[i] <= 0 || M[i] % 64 || K[i] % 256 || (M[i] / 64) * (K[i] / 256) > 0x7FFFFFFF / 8) return -1;
+    FloorItem& it = g.item[i];
+    it.x = static_cast<const uint16_t*>(x[i]);
+    it.row_q = static_cast<uint32_t*>(row_q[i]);
+    it.row_s = static_cast<uint8_t*>(row_s[i]);
+    it.col_q = static_cast<uint8_t*>(col_q[i]);
+    it.col_s = static_cast<uint8_t*>(col_s[i]);
+    it.M = M[i];
+    it.K = K[i];
+    it.tiles_m = (int)(M[i] / 64);
+    it.tiles = it.tiles_m * (int)(K[i] / 256);
+    it.per_xcd = (it.tiles + 7) / 8;
+    slots += it.per_xcd;
+  }
+  if (slots > 0x7FFFFFFF / 8) return -1;
+  hipLaunchKernelGGL(scm ? dual_grouped_floor<1> : dual_grouped_floor<0>, dim3((unsigned)(slots * 8)), dim3(512), 0,
+                     stream, g);
   return (int)hipGetLastError();
 }
 

@@ -168,7 +168,7 @@ def test_bench_floor_library_exports_and_shape_checks():
     # and shapes they do not cover are refused on the host before any launch
     lib = ctypes.CDLL(os.path.join(ROOT, "mxfp4-hopper_amd", "lib", "libomo_ceiling.so"))
     for name in ["omo_ceiling_launch", "omo_floor_dual", "omo_floor_dual_variant", "omo_floor_rowcol", "omo_floor_msplit",
-                 "omo_floor_msplit_band", "omo_floor_requant", "omo_floor_dequant"]:
+                 "omo_floor_msplit_band", "omo_floor_requant", "omo_floor_dequant", "omo_floor_dual_grouped"]:
         assert hasattr(lib, name), name
     P, I64 = ctypes.c_void_p, ctypes.c_int64
     lib.omo_floor_dual.argtypes = [P, P, P, P, P, I64, I64, P]
@@ -194,6 +194,16 @@ def test_bench_floor_library_exports_and_shape_checks():
     assert lib.omo_floor_msplit_band(None, None, None, None, 7168, None, None, None, 8, 4353, None) == -1
     assert lib.omo_floor_msplit_band(None, None, None, None, 7168 + 32, None, None, None, 8, 2000, None) == -1
     assert lib.omo_floor_msplit_band(None, None, None, None, 7168, None, None, None, 0, 2000, None) == -1
+    # grouped: at most 32 items, each M % 64 == 0 and K % 256 == 0, scm 0 or 1
+    lib.omo_floor_dual_grouped.argtypes = [ctypes.c_int, P, P, P, P, P, P, P, ctypes.c_int, P]
+    ptrs = (ctypes.c_void_p * 2)(None, None)
+    ms, ks = (ctypes.c_int64 * 2)(7168, 2048), (ctypes.c_int64 * 2)(2048, 7168)
+    bad_m, bad_k = (ctypes.c_int64 * 2)(7168, 2048 + 32), (ctypes.c_int64 * 2)(2048, 7168 + 128)
+    assert lib.omo_floor_dual_grouped(2, ptrs, ptrs, ptrs, ptrs, ptrs, ms, ks, 2, None) == -1
+    assert lib.omo_floor_dual_grouped(0, ptrs, ptrs, ptrs, ptrs, ptrs, ms, ks, 0, None) == -1
+    assert lib.omo_floor_dual_grouped(0, ptrs, ptrs, ptrs, ptrs, ptrs, ms, ks, 33, None) == -1
+    assert lib.omo_floor_dual_grouped(0, ptrs, ptrs, ptrs, ptrs, ptrs, bad_m, ks, 2, None) == -1
+    assert lib.omo_floor_dual_grouped(1, ptrs, ptrs, ptrs, ptrs, ptrs, ms, bad_k, 2, None) == -1
 
 
 def test_payload_validation_paths():
