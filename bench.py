@@ -51,6 +51,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="comma list of extra legs: dequant,cfg1,payload,ep_payload,permute,moe,msplit,dual,rowcol,"
+                         "rowcol_partial,"
                          "ceiling,floors ('floors' runs only when named); 'headline' runs the headline "
                          "quantize alone")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -761,6 +762,62 @@ def main():
         out["row_to_col_fp8"] = {"workload": "MXFP4 rowwise -> FP8 columnwise 4096x7168",
                                  "kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
                                  "us_per_launch": round(t / steps * 1e3, 2)}
+        del q5, s5, o5, os5
+
+    if want("rowcol_partial"):
+        # a width that is a multiple of 32 but not of 256 (the 256-column tiles' last band
+        # partial): dense 4096 x 7040, and cfg5's routed rows x 7040 in their 8 splits
+        Mr, Nr = 4096, 7040
+        rs_ = sets_for(wl.row_to_col_fp8_bytes(Mr, Nr), args.sets)
+        xq = wl.normal_bf16((Mr, Nr), seed=56, device=dev)
+        qd = [torch.empty((Mr, Nr // 2), dtype=torch.uint8, device=dev) for _ in range(rs_)]
+        sd = [torch.empty((Mr, Nr // 32), dtype=torch.uint8, device=dev) for _ in range(rs_)]
+        for i in range(rs_):
+            omo.omo_per_token_group_quant_fp4(xq, qd[i], sd[i], 32, 1e-10, -6.0, 6.0, False)
+        del xq
+        od = [torch.empty((Nr, Mr), dtype=torch.float8_e4m3fn, device=dev) for _ in range(rs_)]
+        osd = [torch.empty((Mr // 128, Nr), dtype=torch.float32, device=dev) for _ in range(rs_)]
+
+        def rowcol_p(i):
+            _abi.check(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col(
+                qd[i].data_ptr(), Mr, Nr // 2, sd[i].data_ptr(), Mr, Nr // 32, od[i].data_ptr(), Nr, Mr,
+                osd[i].data_ptr(), Mr // 128, Nr, 1e-10, cur()))
+        steps = max(100, args.steps // 4)
+        t, _ = time_launches(torch, rowcol_p, rs_, steps, 20)
+        b = wl.row_to_col_fp8_bytes(Mr, Nr)
+        res = {"dense_workload": "MXFP4 rowwise -> FP8 columnwise 4096x7040",
+               "dense_kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
+               "dense_us_per_launch": round(t / steps * 1e3, 2)}
+        del qd, sd, od, osd
+        c5 = wl.CFG5
+        m_e = wl.moe_routing(c5["tokens"], c5["n_experts"], c5["topk"], range(c5["local_experts"]), seed=5)
+        R = sum(m_e)
+        b = sum(wl.row_to_col_fp8_bytes(m, Nr) for m in m_e)
+        ms_sets = sets_for(b, 3)
+        lens7, offs7, soffs7, mx7 = (torch.tensor(v, dtype=torch.int32, device=dev) if i < 3 else v
+                                     for i, v in enumerate(_split_meta(m_e)))
+        srows7 = sum(-(-m // 128) for m in m_e)
+        xq = wl.normal_bf16((R, Nr), seed=71, device=dev)
+        q7 = [torch.empty((R, Nr // 2), dtype=torch.uint8, device=dev) for _ in range(ms_sets)]
+        s7 = [torch.empty((R, Nr // 32), dtype=torch.uint8, device=dev) for _ in range(ms_sets)]
+        for i in range(ms_sets):
+            omo.omo_per_token_group_quant_fp4(xq, q7[i], s7[i], 32, 1e-10, -6.0, 6.0, False)
+        del xq
+        o7 = [torch.empty((R * Nr,), dtype=torch.uint8, device=dev) for _ in range(ms_sets)]
+        os7 = [torch.empty((srows7, Nr), dtype=torch.float32, device=dev) for _ in range(ms_sets)]
+
+        def msplit_p(i):
+            _abi.check(lib.omo_hip_per_token_Mxfp4RowToBf16ToFp8Col_msplit(
+                q7[i].data_ptr(), R, Nr // 2, s7[i].data_ptr(), s7[i].numel(), o7[i].data_ptr(), o7[i].numel(),
+                os7[i].data_ptr(), os7[i].numel(), lens7.data_ptr(), offs7.data_ptr(), soffs7.data_ptr(), len(m_e),
+                mx7, 1e-10, cur()))
+        steps = max(50, args.steps // 10)
+        t, _ = time_launches(torch, msplit_p, ms_sets, steps, 10)
+        res.update({"msplit_workload": f"per-split, cfg5's {R} routed rows x {Nr} in {len(m_e)} splits",
+                    "msplit_kernel_GB/s": round(b / (t / steps * 1e-3) / 1e9, 1),
+                    "msplit_us_per_launch": round(t / steps * 1e3, 2)})
+        out["row_to_col_partial_band"] = res
+        del q7, s7, o7, os7
 
     if want("msplit"):
         # cfg5's per-split row -> col FP8 alone (the moe leg runs it after the grouped weight

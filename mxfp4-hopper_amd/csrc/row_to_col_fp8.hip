@@ -18,10 +18,11 @@
 // out_s = 1/scale at [(soff_i + tile) * N + c], q = v * scale, and the
 // split's output block [N, len_i] starts at off_i * N.
 //
-// Two tile shapes. Where N % 256 == 0 (with 16 B aligned codes and 8 B
-// aligned scales) tiles are 128 rows x 256 element columns, one 256-thread
-// workgroup each, a lane per code dword (wide_tile, below), for any M. Other
-// shapes take 128 x 128 tiles, one 512-thread block per tile, described here.
+// Two tile shapes. Where N % 32 == 0 and the codes are 16 B aligned, tiles
+// are 128 rows x 256 element columns (the last band partial when N % 256 !=
+// 0), one 256-thread workgroup each, a lane per code dword (wide_tile,
+// below), for any M. Other inputs (codes not 16 B aligned, N % 32 != 0)
+// take 128 x 128 tiles, one 512-thread block per tile, described here.
 // The tile's code bytes (128 rows x 64 B) and
 // scale bytes are staged in LDS. Lane t owns code-byte column p = t/8 (two
 // element columns) and the 16 rows of eighth q = t%8, so 8 adjacent lanes
@@ -442,8 +443,8 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_kernel(const uint8_
   }
 }
 
-// Tiles of 128 rows x 256 element columns (N % 256 == 0, 16 B aligned codes,
-// 8 B aligned scales), one 256-thread workgroup per tile. Lane t owns code
+// Tiles of 128 rows x 256 element columns (16 B aligned codes, N % 32 == 0;
+// the last band partial when N % 256 != 0), one 256-thread workgroup per tile. Lane t owns code
 // bytes 4c .. 4c+3 (element columns 8c .. 8c+7, one MX column), c = t / 8,
 // and rows 16q .. 16q+15, q = t % 8: per row it reads one code dword from
 // LDS (instead of one byte per two element columns), the 8 lanes of a code
@@ -682,12 +683,19 @@ __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, co
 // the neighbouring tiles of the column) are completed in L2, unless line_nt
 // says every column piece of the tile is one whole 128 B line. Not RAGGED:
 // rows_valid == 128 and 16 B aligned non-temporal stores.
-template <bool MSPLIT, bool RAGGED>
+// SBYTE: the 8 scale bytes of a tile row are read one by one (rows of N / 32
+// scale bytes that are not 8 B aligned, N % 256 != 0). PARTIAL: only element
+// columns col0 .. col0 + cols_valid - 1 exist (the last band when N % 256 !=
+// 0; cols_valid a multiple of 32): the missing 16 B code chunks of a row read
+// its last chunk and are zeroed, their scale bytes read as 127, and the lanes
+// of the missing columns store nothing.
+template <bool MSPLIT, bool RAGGED, bool PARTIAL = false, bool SBYTE = false>
 __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
                                           int64_t N, int64_t row0, int rows_valid, int64_t col0, float eps,
                                           float* __restrict__ out_s_row, uint8_t* __restrict__ obase, int64_t cstride,
-                                          bool line_nt) {
+                                          bool line_nt, int cols_valid = kWideCols) {
   const int t = threadIdx.x;
+  const int nch = PARTIAL ? cols_valid / 32 : 8;  // code chunks (and MX columns) per tile row
   // ---- stage codes (1024 chunks of 16 B, 8 rows x 128 B per wave load) and scales.
   // RAGGED: a row past rows_valid loads the tile's last row (in bounds, lines
   // the tile reads anyway) and is replaced by codes 0 / scale 127 afterwards,
@@ -699,17 +707,28 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   for (int k = 0; k < 4; k++) {
     const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
     const int rr = RAGGED ? min(r, rows_valid - 1) : r;
-    cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + rr) * (N / 2) + col0 / 2 + c16 * 16);
+    const int cc = PARTIAL ? min(c16, nch - 1) : c16;
+    cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + rr) * (N / 2) + col0 / 2 + cc * 16);
   }
   u32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
-  if (t < kTile) sv = *reinterpret_cast<const u32x2*>(s + (row0 + (RAGGED ? min(t, rows_valid - 1) : t)) * (N / 32) + col0 / 32);
-  if (RAGGED) {
+  if (t < kTile) {
+    const uint8_t* srow = s + (row0 + (RAGGED ? min(t, rows_valid - 1) : t)) * (N / 32) + col0 / 32;
+    if (SBYTE) {
+      uint32_t w[2] = {0u, 0u};
+#pragma unroll
+      for (int c = 0; c < 8; c++) w[c >> 2] |= (c < nch ? (uint32_t)srow[c] : 0x7Fu) << (8 * (c & 3));
+      sv = u32x2{w[0], w[1]};
+    } else {
+      sv = *reinterpret_cast<const u32x2*>(srow);
+    }
+  }
+  if (RAGGED || PARTIAL) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const int r = (t + 256 * k) >> 3;
-      if (r >= rows_valid) cv[k] = u32x4{0u, 0u, 0u, 0u};
+      const int r = (t + 256 * k) >> 3, c16 = (t + 256 * k) & 7;
+      if ((RAGGED && r >= rows_valid) || (PARTIAL && c16 >= nch)) cv[k] = u32x4{0u, 0u, 0u, 0u};
     }
-    if (t >= rows_valid) sv = u32x2{0x7F7F7F7Fu, 0x7F7F7F7Fu};
+    if (RAGGED && t >= rows_valid) sv = u32x2{0x7F7F7F7Fu, 0x7F7F7F7Fu};
   }
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -726,44 +745,65 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   }
   __syncthreads();
   const int qq = t & 7, cg = t >> 3, mx = cg >> 2;
+  const bool col_ok = !PARTIAL || mx < nch;  // this lane's 8 element columns exist
   uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
-  wide_convert<MSPLIT>(sm.codes, kWidePitch, sm.scales[mx], sm.fscales[mx], cg, qq, eps, true, out_s_row + 8 * cg + qq,
-                       [&](int e, const u32x4& w) {
+  wide_convert<MSPLIT>(sm.codes, kWidePitch, sm.scales[mx], sm.fscales[mx], cg, qq, eps, col_ok,
+                       out_s_row + 8 * cg + qq, [&](int e, const u32x4& w) {
+                         if (PARTIAL && !col_ok) return;
                          if (RAGGED && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);
                          else __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(o + e * cstride));
                        });
 }
 
-// Dense, N % 256 == 0, tile (bm, bn) = blockIdx renumbered per XCD, bn
-// fastest. Not RAGGED: whole aligned tiles (M % 128 == 0, 16 B aligned
-// output). RAGGED: any M, any output alignment (the last row tile partial).
-template <bool RAGGED>
+// A tile of band col0 / 256: the whole band, or (NARROWN, N % 256 != 0)
+// the last band's N - col0 columns.
+template <bool MSPLIT, bool RAGGED, bool NARROWN>
+__device__ __forceinline__ void wide_tile_any(WideSmem& sm, const uint8_t* __restrict__ q,
+                                              const uint8_t* __restrict__ s, int64_t N, int64_t row0, int rows_valid,
+                                              int64_t col0, float eps, float* __restrict__ out_s_row,
+                                              uint8_t* __restrict__ obase, int64_t cstride, bool line_nt) {
+  if (!NARROWN || col0 + kWideCols <= N) {
+    wide_tile<MSPLIT, RAGGED, false, NARROWN>(sm, q, s, N, row0, rows_valid, col0, eps, out_s_row, obase, cstride,
+                                              line_nt);
+  } else {
+    wide_tile<MSPLIT, RAGGED, true, NARROWN>(sm, q, s, N, row0, rows_valid, col0, eps, out_s_row, obase, cstride,
+                                             line_nt, (int)(N - col0));
+  }
+}
+
+// Dense, tile (bm, bn) = blockIdx renumbered per XCD, bn fastest. Not
+// RAGGED: whole aligned tiles (M % 128 == 0, 16 B aligned output). RAGGED:
+// any M, any output alignment (the last row tile partial). NARROWN: N % 32
+// == 0 but not a multiple of 256, or scale rows not 8 B aligned (the last
+// band partial, scale bytes read one by one).
+template <bool RAGGED, bool NARROWN>
 __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8_t* __restrict__ q,
                                                                      const uint8_t* __restrict__ s,
                                                                      uint8_t* __restrict__ out,
                                                                      float* __restrict__ out_s, int64_t M, int64_t N,
                                                                      float eps) {
   __shared__ WideSmem sm;
-  const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)(N / kWideCols);
+  const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)((N + kWideCols - 1) / kWideCols);
   const int64_t bn = L % gx, bm = L / gx;
   const int64_t row0 = bm * kTile, col0 = bn * kWideCols;
   const int rows_valid = RAGGED ? (int)(M - row0 < kTile ? M - row0 : kTile) : kTile;
-  wide_tile<false, RAGGED>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + bm * N + col0, out + col0 * M + row0, M,
-                           false);
+  wide_tile_any<false, RAGGED, NARROWN>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + bm * N + col0,
+                                        out + col0 * M + row0, M, false);
 }
 
-// Per split, N % 256 == 0: workgroup (split, bm, bn) as in
-// row_to_fp8_col_msplit_kernel. A split whose length is a multiple of 128
-// (start * N is a multiple of 256 already) has every column piece on one
-// whole 128 B line when the output base is 128 B aligned (out_line): those
-// tiles store non-temporally (30.9 us against 43.0 us with ordinary stores
-// over 8 such splits of 7168 columns); the others keep ordinary stores,
-// since non-temporal partial lines are not merged in L2 (ragged splits took
-// 81.4 us that way against 58.2 us).
+// Per split on the 256-column tiles: workgroup (split, bm, bn) as in
+// row_to_fp8_col_msplit_kernel. A split whose length and block start
+// start * N are multiples of 128 (the start always is when N % 128 == 0) has
+// every column piece on one whole 128 B line when the output base is 128 B
+// aligned (out_line): those tiles store non-temporally (30.9 us against 43.0
+// us with ordinary stores over 8 such splits of 7168 columns); the others
+// keep ordinary stores, since non-temporal partial lines are not merged in L2
+// (ragged splits took 81.4 us that way against 58.2 us).
 // Row tile bm, column band bn of a split with rows [start, start + len) and
 // scale rows from sstart. Metadata arrives on the device; tiles whose rows
 // or scale rows fall outside the buffers are skipped rather than written out
 // of bounds. Uniform over the workgroup.
+template <bool NARROWN>
 __device__ __forceinline__ void msplit_wide_tile(WideSmem& sm, const uint8_t* __restrict__ q,
                                                  const uint8_t* __restrict__ s, uint8_t* __restrict__ out,
                                                  float* __restrict__ out_s, int64_t len, int64_t start, int64_t sstart,
@@ -773,10 +813,12 @@ __device__ __forceinline__ void msplit_wide_tile(WideSmem& sm, const uint8_t* __
   if (start < 0 || start + len > total_rows || sstart < 0 || sstart + bm >= out_s_rows) return;
   const int64_t row0 = start + bm * kTile, col0 = bn * kWideCols;
   const int rows_valid = (int)(len - bm * kTile < kTile ? len - bm * kTile : kTile);
-  wide_tile<true, true>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + (sstart + bm) * N + col0,
-                  out + start * N + col0 * len + bm * kTile, len, out_line && len % kTile == 0);
+  wide_tile_any<true, true, NARROWN>(sm, q, s, N, row0, rows_valid, col0, eps, out_s + (sstart + bm) * N + col0,
+                                     out + start * N + col0 * len + bm * kTile, len,
+                                     out_line && len % kTile == 0 && (start * N) % kTile == 0);
 }
 
+template <bool NARROWN>
 __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_wide_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
@@ -785,7 +827,7 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_wide_kernel(
   const int64_t split = blockIdx.x, bm = bm0 + blockIdx.y, bn = bn0 + blockIdx.z;
   const int64_t len = lens[split];
   if (bm * kTile >= len) return;
-  msplit_wide_tile(sm, q, s, out, out_s, len, offs[split], soffs[split], bm, bn, total_rows, N, out_s_rows, eps,
+  msplit_wide_tile<NARROWN>(sm, q, s, out, out_s, len, offs[split], soffs[split], bm, bn, total_rows, N, out_s_rows, eps,
                    out_line);
 }
 
@@ -826,9 +868,11 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
 // against 55.4 us for 8 splits (1801..2279 rows), 49.5/54.9 for 4 uneven,
 // 51.0/53.9 for 16, 51.2/52.7 for 32; past 64 splits the ranges win (53.9
 // against 54.3 us at 65, 56.1/57.3 at 100, 60.1/61.7 at 128). The wide
-// kernel walks bands up to 64 splits. With the 128-column tiles (N = 7040)
-// the ranges win at every count (70.0 against 79.4 us at 8 splits, 82.0/91.0
-// at 16) and are always used.
+// kernel walks bands up to 64 splits, also with a partial last band (N =
+// 7040: 50.5-52.7 us for 4 to 32 splits, 51.1 for 8 nearly equal ones). The
+// 128-column tiles (codes not 16 B aligned) keep the ranges, which won there
+// at every count (N = 7040: 70.0 against 79.4 us at 8 splits, 82.0/91.0 at
+// 16).
 // On the 3-D grid (split, row tile, band) a split's tiles all land on one
 // XCD when the split count is a multiple of 8 (the XCD holding the longest
 // splits then finishes last) and are scattered otherwise. On 16431 routed
@@ -949,7 +993,7 @@ __device__ __forceinline__ bool flat_split_tile(const int32_t* __restrict__ lens
   return true;
 }
 
-template <int CHUNKS>
+template <int CHUNKS, bool NARROWN>
 __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
@@ -958,7 +1002,7 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
   int64_t len, start, sstart, bm, bn;
   if (!flat_split_tile<CHUNKS, CHUNKS == 1>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn))
     return;
-  msplit_wide_tile(sm, q, s, out, out_s, len, start, sstart, bm, bn, total_rows, N, out_s_rows, eps, out_line);
+  msplit_wide_tile<NARROWN>(sm, q, s, out, out_s, len, start, sstart, bm, bn, total_rows, N, out_s_rows, eps, out_line);
 }
 
 // A split's output column c is a run of len bytes at off*N + c*len, so a
@@ -1006,11 +1050,12 @@ __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_kernel(
 }
 
 // The 128-column tiles on the flat grid (at most 128 splits), as the wide
-// form. On 16431 routed rows x 7040 columns: 4, 16 and 32 uneven splits
-// 71.4, 96.2 and 85.8 us against 94.1, 313.3 and 177.7 us on the 3-D grid;
-// cfg5's 8 nearly equal splits 71.3 against 65.8 us (the tile search of
-// twice as many 512-thread workgroups costs more than the 3-D grid's one
-// split per XCD, which any imbalance above about 8% undoes).
+// form, for codes that are not 16 B aligned. On 16431 routed rows x 7040
+// columns: 4, 16 and 32 uneven splits 71.4, 96.2 and 85.8 us against 94.1,
+// 313.3 and 177.7 us on the 3-D grid; cfg5's 8 nearly equal splits 71.3
+// against 65.8 us (the tile search of twice as many 512-thread workgroups
+// costs more than the 3-D grid's one split per XCD, which any imbalance
+// above about 8% undoes).
 template <int CHUNKS>
 __global__ __launch_bounds__(kRcThreads) void row_to_fp8_col_msplit_narrow_flat_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
@@ -1029,11 +1074,18 @@ hipError_t launch_row_to_fp8_col(const void* q, const void* s, void* out, float*
   const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
   const bool vout = (M % 16 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
   const bool full = vin && vs && vout && (M % kTile == 0);
-  if (vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0) {
-    const dim3 grid((unsigned)(((M + kTile - 1) / kTile) * (N / kWideCols)));
-    auto kernel = full ? row_to_fp8_col_wide_kernel<false> : row_to_fp8_col_wide_kernel<true>;
+  if (vin) {
+    // the 256-column tiles; their scale rows are read 8 bytes at a time when
+    // 8 B aligned (N % 256 == 0), else byte by byte with the last band
+    // partial. 4096 x 7040: 9.5 us against 12.6 us on the 128-column tiles;
+    // 16384 x 7040: 29.2 against 56.0; 4096 x 2880: 5.6 against 8.4.
+    const bool narrow_n = N % kWideCols != 0 || (reinterpret_cast<uintptr_t>(s) & 7) != 0;
+    const bool whole = vout && M % kTile == 0;
+    const dim3 grid((unsigned)(((M + kTile - 1) / kTile) * ((N + kWideCols - 1) / kWideCols)));
+    auto kernel = narrow_n ? (whole ? row_to_fp8_col_wide_kernel<false, true> : row_to_fp8_col_wide_kernel<true, true>)
+                           : (whole ? row_to_fp8_col_wide_kernel<false, false> : row_to_fp8_col_wide_kernel<true, false>);
     return launch(kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s),
-                       static_cast<uint8_t*>(out), out_s, M, N, eps);
+                  static_cast<uint8_t*>(out), out_s, M, N, eps);
   }
   const int64_t tiles_m = (M + kTile - 1) / kTile, tiles = tiles_m * ((N + kTile - 1) / kTile);
   // one wave of resident blocks: two 512-thread blocks per CU at this
@@ -1054,9 +1106,10 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   if (nsplits == 0 || max_split_len <= 0 || N == 0) return hipSuccess;
   const bool vin = (N % 32 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
   const bool vs = (N % 128 == 0) && ((reinterpret_cast<uintptr_t>(s) & 3) == 0);
-  const bool wide = vin && N % kWideCols == 0 && (reinterpret_cast<uintptr_t>(s) & 7) == 0;
+  const bool wide = vin;  // 256-column tiles (the last band partial where N % 256 != 0)
+  const bool narrow_n = N % kWideCols != 0 || (reinterpret_cast<uintptr_t>(s) & 7) != 0;
   const int64_t tiles_m = (max_split_len + kTile - 1) / kTile;
-  const int64_t bands = wide ? N / kWideCols : (N + kTile - 1) / kTile;
+  const int64_t bands = wide ? (N + kWideCols - 1) / kWideCols : (N + kTile - 1) / kTile;
   // Unused dynamic LDS caps the wide kernel's residency at 4 workgroups per
   // CU (6 by its own LDS and registers): fewer tiles' partial output lines
   // wait in L2 at once. Ragged cfg5 splits: 49.6 us against 51.0, and 59.8
@@ -1070,7 +1123,10 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   if (nsplits <= kFlatMaxSplits && tiles_m * bands + 7 <= (int64_t)UINT32_MAX / flat_threads / nsplits) {
     const dim3 grid((unsigned)flat_grid_blocks(nsplits, tiles_m, bands));
     if (wide) {
-      auto kernel = nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1> : row_to_fp8_col_msplit_flat_kernel<2>;
+      auto kernel = narrow_n ? (nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1, true>
+                                              : row_to_fp8_col_msplit_flat_kernel<2, true>)
+                             : (nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1, false>
+                                              : row_to_fp8_col_msplit_flat_kernel<2, false>);
       return launch(kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
                     static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
                     out_s_rows, eps, out_line, (int)nsplits, (int)tiles_m, (int)bands);
@@ -1087,7 +1143,8 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
       const dim3 grid((unsigned)nsplits, (unsigned)std::min<int64_t>(tiles_m - bm0, kMaxGridYZ),
                       (unsigned)std::min<int64_t>(bands - bn0, kMaxGridYZ));
       const hipError_t e =
-          wide ? launch(row_to_fp8_col_msplit_wide_kernel, grid, dim3(256), reserve, stream,
+          wide ? launch(narrow_n ? row_to_fp8_col_msplit_wide_kernel<true> : row_to_fp8_col_msplit_wide_kernel<false>,
+                        grid, dim3(256), reserve, stream,
                         static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out),
                         out_s, lens, offs, soffs, total_rows, N, out_s_rows, eps, out_line, bm0, bn0)
                : launch(row_to_fp8_col_msplit_kernel, grid, dim3(kRcThreads), 0, stream,

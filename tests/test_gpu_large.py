@@ -173,21 +173,30 @@ def test_msplit_more_row_tiles_than_grid_y(oracle, dev, empty_tail):
     np.testing.assert_array_equal(outs[-es.shape[0]:].cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
-@pytest.mark.parametrize("N,empty_tail", [(65536 * 256 + 256, 0), (65536 * 256 + 256, 255), (65536 * 128 + 128, 0),
-                                          (65536 * 128 + 128, 125)])
-def test_msplit_more_column_bands_than_grid_z(oracle, dev, N, empty_tail):
+@pytest.mark.parametrize("N,empty_tail,shift", [(65536 * 256 + 256, 0, 0), (65536 * 256 + 256, 255, 0),
+                                                (65536 * 128 + 128, 0, 4), (65536 * 128 + 128, 125, 4),
+                                                (65536 * 128 + 128, 0, 0)])
+def test_msplit_more_column_bands_than_grid_z(oracle, dev, N, empty_tail, shift):
     """Rows of 16.8M (256-column bands, the wide kernel: on the flat grid,
     and with 255 empty splits appended on the 3-D grid) or 8.4M columns
-    (128-column bands, the general kernel) have more than the 65,536 column
-    bands grid z holds: column windows at the start and across the last band
-    boundaries against the oracle on those columns. With 125 empty splits
-    appended (128 splits, the flat grid's limit) the 128-column flat grid
-    would need 128 x 65,537 workgroups of 512 lanes, past the 2^32 - 1
-    work-items a launch holds along x, so the 3-D grid takes it."""
+    (128-column bands of the general kernel, which codes 4 bytes past a 16 B
+    boundary take) have more than the 65,536 column bands grid z holds:
+    column windows at the start and across the last band boundaries against
+    the oracle on those columns. With 125 empty splits appended (128 splits,
+    the flat grid's limit) the 128-column flat grid would need 128 x 65,537
+    workgroups of 512 lanes, past the 2^32 - 1 work-items a launch holds
+    along x, so the 3-D grid takes it. The same 8.4M columns with aligned
+    codes take the 256-column bands with a partial last band."""
     splits = [128, 1, 77] + [0] * empty_tail
     R = sum(splits)
-    _say("msplit wide rows", splits, N)
+    _say("msplit wide rows", splits, N, shift)
     q, s = _gpu_codes(dev, R, N, 35)
+    if shift:
+        flat = torch.empty(q.numel() + 16, dtype=torch.uint8, device=dev)
+        qm = flat[shift:shift + q.numel()].view(q.shape)
+        qm.copy_(q)
+        del q
+        q = qm
     out, outs = _msplit_gpu(dev, q, s, splits)
     for c0, w in ((0, 256), (N - 768, 768)):
         eo, es = oracle.row_to_fp8_col_msplit(bits_u8(q[:, c0 // 2:(c0 + w) // 2]), bits_u8(s[:, c0 // 32:(c0 + w) // 32]),

@@ -428,9 +428,10 @@ def payload_from_normal(M, K, seed, std=1.0):
     return q.reshape(M, K // 2), s.reshape(M, K // 32)
 
 
-# (128, 128) takes the 128-column whole-tile kernel and (1, 64) its ragged
-# form; (256, 256), (512, 7168), (1024, 2048) and (128, 768) the 256-column
-# whole-tile kernel; (300, 7168), (129, 4096) and (1000, 2048) its ragged form.
+# (128, 128) takes the 256-column tiles with a partial band (128 columns) and
+# (1, 64) its ragged form; (256, 256), (512, 7168), (1024, 2048) and (128,
+# 768) the whole 256-column tiles; (300, 7168), (129, 4096) and (1000, 2048)
+# their ragged form.
 @pytest.mark.parametrize("M,N,seed", [(128, 128, 1), (300, 7168, 2), (1, 64, 3), (129, 4096, 4), (1000, 2048, 5),
                                       (256, 256, 6), (512, 7168, 7), (1024, 2048, 8), (128, 768, 9)])
 def test_row_to_fp8_col_dense(oracle, dev, M, N, seed):
@@ -497,15 +498,16 @@ def test_row_to_fp8_col_wide_scales(oracle, dev):
     np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
 
 
-@pytest.mark.parametrize("N", [512, 384])
+@pytest.mark.parametrize("N,shift", [(512, 0), (384, 0), (384, 4)])
 @pytest.mark.parametrize("eps", [-1.0, -0.0, 1e-10])
-def test_row_to_fp8_col_nan_lane_groups(oracle, dev, N, eps):
+def test_row_to_fp8_col_nan_lane_groups(oracle, dev, N, shift, eps):
     """Lanes whose values are all NaN: codes 0 with scale byte 255 (0 * inf)
     over whole 16-row lane groups, so that with eps negative a lane's column
     maximum stays eps (< 0) and the kernels reduce the maxima with fmaxf
     rather than as integers; eps -0.0 keeps -0.0 maxima. N = 512 takes the
-    256-column tiles, N = 384 the 128-column ones."""
-    _say("row_to_fp8_col nan lane groups", N, eps)
+    256-column tiles, N = 384 the same with a partial band, and N = 384 with
+    codes 4 bytes past a 16 B boundary the 128-column ones."""
+    _say("row_to_fp8_col nan lane groups", N, shift, eps)
     omo = _omo()
     rng = np.random.default_rng(N)
     M = 256
@@ -517,7 +519,8 @@ def test_row_to_fp8_col_nan_lane_groups(oracle, dev, N, eps):
     s[128:256, 2] = 255
     out = torch.empty((N, M), dtype=FP8, device=dev)
     outs = torch.empty((M // 128, N), dtype=torch.float32, device=dev)
-    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, eps)
+    qd = _misaligned(dev, q, shift) if shift else torch.from_numpy(q).to(dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(qd, torch.from_numpy(s).to(dev), out, outs, eps)
     torch.cuda.synchronize()
     eo, es = oracle.row_to_fp8_col(q, s, eps=eps)
     np.testing.assert_array_equal(bits_u8(out), eo)
@@ -579,8 +582,8 @@ def test_row_to_fp8_col_msplit(oracle, dev, splits, N):
 
 
 # Lengths 17i (i = 1..15) end a tile's column piece after every count 1..15
-# of bytes of a 16-row block, on the 256-column kernel (N = 256) and the
-# 128-column one (N = 384). Lengths that are multiples of 128 among ragged
+# of bytes of a 16-row block, on whole 256-column bands (N = 256) and with a
+# partial last band (N = 384). Lengths that are multiples of 128 among ragged
 # ones (N = 512) mix line-aligned tiles (non-temporal stores) with the others.
 @pytest.mark.parametrize("splits,N", [([211, 97, 300, 5, 256, 130], 7168), ([2083, 17, 1965], 1024),
                                       ([129, 255, 383, 1, 16, 144], 384), ([17 * i for i in range(1, 16)], 256),
@@ -618,6 +621,84 @@ def _msplit_sentinel_run(dev, q, s, splits, N, max_len=None):
     return bits_u8(out_q), out_s.cpu().numpy().view(np.uint32)
 
 
+def _misaligned(dev, a, shift):
+    """A device copy of a at a byte address `shift` past a 256 B boundary."""
+    flat = torch.empty(a.size + 256, dtype=torch.uint8, device=dev)
+    v = flat[shift:shift + a.size].view(a.shape)
+    v.copy_(torch.from_numpy(a))
+    assert v.data_ptr() % 16 == shift % 16
+    return v
+
+
+# Widths that are multiples of 32 but not of 256 take the 256-column tiles
+# with a partial last band (N - 256 * (N // 256) columns) and scale rows read
+# byte by byte; outputs pre-filled with a sentinel.
+@pytest.mark.parametrize("M,N", [(300, 7040), (128, 2880), (1, 96), (257, 160), (512, 1056), (4096, 7040)])
+def test_row_to_fp8_col_partial_band(oracle, dev, M, N):
+    omo = _omo()
+    _say("row_to_fp8_col partial band", M, N)
+    q, s = payload_from_normal(M, N, M + N)
+    out = torch.full((N, M), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    outs = torch.full(((M + 127) // 128, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+@pytest.mark.parametrize("nsplits,N,seed", [(8, 7040, 1), (5, 2880, 2), (3, 160, 3), (100, 2880, 4), (200, 1056, 5),
+                                            (1, 96, 6)])
+def test_row_to_fp8_col_msplit_partial_band(oracle, dev, nsplits, N, seed):
+    """Per split on the 256-column tiles with a partial last band: the flat
+    grid at up to 64 splits (band walk) and up to 128, the 3-D grid past 128."""
+    rng = np.random.default_rng(seed)
+    splits = [int(v) for v in rng.choice([0, 1, 17, 127, 128, 129, 300, 700, 2050], size=nsplits)]
+    if sum(splits) == 0:
+        splits[-1] = 129
+    _say("msplit partial band", nsplits, N, sum(splits))
+    q, s = payload_from_normal(sum(splits), N, seed)
+    got, got_s = _msplit_sentinel_run(dev, q, s, splits, N)
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(got, eo)
+    np.testing.assert_array_equal(got_s, es.view(np.uint32))
+
+
+# Code rows at an address that is not 16 B aligned take the 128-column
+# kernels (byte-wise code loads); the scales at an odd address too.
+@pytest.mark.parametrize("M,N,shift", [(300, 7168, 4), (128, 384, 8), (1, 64, 1), (700, 2048, 12)])
+def test_row_to_fp8_col_misaligned_codes(oracle, dev, M, N, shift):
+    omo = _omo()
+    _say("row_to_fp8_col misaligned codes", M, N, shift)
+    q, s = payload_from_normal(M, N, M * 5 + N)
+    out = torch.full((N, M), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    outs = torch.full(((M + 127) // 128, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(_misaligned(dev, q, shift), _misaligned(dev, s, 3), out, outs, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+@pytest.mark.parametrize("splits,N,shift", [([129, 255, 17], 384, 4), ([5, 300, 128, 0, 1], 7168, 8),
+                                            ([1] * 70 + [300], 512, 2)])
+def test_row_to_fp8_col_msplit_misaligned_codes(oracle, dev, splits, N, shift):
+    import omo
+    from omo_python_api.mxfp4_dequant import split_metadata
+    _say("msplit misaligned codes", len(splits), N, shift)
+    M = sum(splits)
+    q, s = payload_from_normal(M, N, M % 61)
+    lens, offs, soffs, ml, rows, srows = split_metadata(splits, dev)
+    out_q = torch.full((M * N,), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    out_s = torch.full((srows, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col_msplit(_misaligned(dev, q, shift), _misaligned(dev, s, 1), out_q, out_s,
+                                                    lens, offs, soffs, ml, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(bits_u8(out_q), eo)
+    np.testing.assert_array_equal(out_s.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
 @pytest.mark.parametrize("nsplits,N,seed", [(100, 256, 1), (256, 128, 2), (300, 128, 3), (9, 1056, 4), (5, 96, 5)])
 def test_row_to_fp8_col_msplit_many_splits(oracle, dev, nsplits, N, seed):
     """Many splits (the grid's first dimension), N % 128 != 0 (a partial
@@ -641,8 +722,8 @@ def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed, N
     """Split counts on both sides of 64 (one split per lane on the flat grid)
     and of 128 (the flat grid's limit; 129 and 256 take the 3-D grid) with
     very uneven lengths (empty, one-row, ragged and long splits), into
-    sentinel-filled outputs: N = 512 (two 256-column bands), N = 384 (three
-    bands of the 128-column kernel)."""
+    sentinel-filled outputs: N = 512 (two 256-column bands), N = 384 (a
+    whole band and a partial one)."""
     rng = np.random.default_rng(seed)
     splits = [int(v) for v in rng.choice([0, 1, 17, 127, 128, 129, 300, 700, 1500], size=nsplits)]
     if sum(splits) == 0:
@@ -655,8 +736,9 @@ def test_row_to_fp8_col_msplit_uneven_split_counts(oracle, dev, nsplits, seed, N
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
-@pytest.mark.parametrize("N,extra", [(512, 0), (512, 66), (512, 260), (384, 0), (384, 260)])
-def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
+@pytest.mark.parametrize("N,extra,shift", [(512, 0, 0), (512, 66, 0), (512, 260, 0), (384, 0, 0), (384, 0, 4),
+                                           (384, 260, 4)])
+def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra, shift):
     """Split metadata is read on the device, so the kernels skip tiles whose
     rows or scale rows fall outside the buffers: a split running past the
     last row, one whose scale rows start past output_s, and one with a
@@ -665,9 +747,10 @@ def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
     filled allocation, so a tile that were not skipped would land in the
     padding (checked untouched) instead of outside the allocation. N = 512
     takes the flat grid (extra empty splits: two splits per lane at 66, the
-    3-D grid at 260), N = 384 the 128-column kernel (flat, and 3-D at 260)."""
+    3-D grid at 260), N = 384 a partial band, and N = 384 with the codes 4
+    bytes past a 16 B boundary the 128-column kernel (flat, and 3-D at 260)."""
     import omo
-    _say("msplit bad metadata", N, extra)
+    _say("msplit bad metadata", N, extra, shift)
     valid = [300, 129]
     M = sum(valid)
     srows = sum((m + 127) // 128 for m in valid)
@@ -676,7 +759,8 @@ def test_row_to_fp8_col_msplit_skips_bad_metadata(oracle, dev, N, extra):
     soffs = [0, 0, 3, srows, 0] + [0] * extra
     q, s = payload_from_normal(M, N, 5)
     pad = 256
-    big_q = torch.zeros((M + 2 * pad, N // 2), dtype=torch.uint8, device=dev)
+    big_q = torch.zeros(((M + 2 * pad) * (N // 2) + 16,), dtype=torch.uint8, device=dev)
+    big_q = big_q[shift:shift + (M + 2 * pad) * (N // 2)].view(M + 2 * pad, N // 2)
     big_s = torch.full((M + 2 * pad, N // 32), 127, dtype=torch.uint8, device=dev)
     big_q[pad:pad + M] = torch.from_numpy(q).to(dev)
     big_s[pad:pad + M] = torch.from_numpy(s).to(dev)
