@@ -867,12 +867,15 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
 // On 16431 routed rows x 7168 (wide tiles), band walk against ranges: 49.5
 // against 55.4 us for 8 splits (1801..2279 rows), 49.5/54.9 for 4 uneven,
 // 51.0/53.9 for 16, 51.2/52.7 for 32; past 64 splits the ranges win (53.9
-// against 54.3 us at 65, 56.1/57.3 at 100, 60.1/61.7 at 128). The wide
-// kernel walks bands up to 64 splits, also with a partial last band (N =
-// 7040: 50.5-52.7 us for 4 to 32 splits, 51.1 for 8 nearly equal ones). The
-// 128-column tiles (codes not 16 B aligned) keep the ranges, which won there
-// at every count (N = 7040: 70.0 against 79.4 us at 8 splits, 82.0/91.0 at
-// 16).
+// against 54.3 us at 65, 56.1/57.3 at 100, 60.1/61.7 at 128). On rows of
+// few bands the ranges win (the same rows, 8 splits: N = 2048, 14.3 against
+// 15.9 us; 2880, 19.1 against 22.0; 3072, 19.1 against 20.8; 4096, 29.1
+// against 29.9), on more the band walk (5120, 36.7 against 38.3; 6144, 41.9
+// against 46.9). The wide kernel walks bands up to 64 splits on rows of more
+// than 16 bands, also with a partial last band (N = 7040: 50.5-52.7 us for 4
+// to 32 splits, 51.1 for 8 nearly equal ones). The 128-column tiles (codes
+// not 16 B aligned) keep the ranges, which won there at every count (N =
+// 7040: 70.0 against 79.4 us at 8 splits, 82.0/91.0 at 16).
 // On the 3-D grid (split, row tile, band) a split's tiles all land on one
 // XCD when the split count is a multiple of 8 (the XCD holding the longest
 // splits then finishes last) and are scattered otherwise. On 16431 routed
@@ -993,15 +996,14 @@ __device__ __forceinline__ bool flat_split_tile(const int32_t* __restrict__ lens
   return true;
 }
 
-template <int CHUNKS, bool NARROWN>
+template <int CHUNKS, bool WALK, bool NARROWN>
 __global__ __launch_bounds__(256, 4) void row_to_fp8_col_msplit_flat_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ s, uint8_t* __restrict__ out, float* __restrict__ out_s,
     const int32_t* __restrict__ lens, const int32_t* __restrict__ offs, const int32_t* __restrict__ soffs,
     int64_t total_rows, int64_t N, int64_t out_s_rows, float eps, bool out_line, int nsplits, int tm, int bands) {
   __shared__ WideSmem sm;
   int64_t len, start, sstart, bm, bn;
-  if (!flat_split_tile<CHUNKS, CHUNKS == 1>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn))
-    return;
+  if (!flat_split_tile<CHUNKS, WALK>(lens, offs, soffs, nsplits, tm, bands, &len, &start, &sstart, &bm, &bn)) return;
   msplit_wide_tile<NARROWN>(sm, q, s, out, out_s, len, start, sstart, bm, bn, total_rows, N, out_s_rows, eps, out_line);
 }
 
@@ -1123,10 +1125,14 @@ hipError_t launch_row_to_fp8_col_msplit(const void* q, const void* s, void* out,
   if (nsplits <= kFlatMaxSplits && tiles_m * bands + 7 <= (int64_t)UINT32_MAX / flat_threads / nsplits) {
     const dim3 grid((unsigned)flat_grid_blocks(nsplits, tiles_m, bands));
     if (wide) {
-      auto kernel = narrow_n ? (nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1, true>
-                                              : row_to_fp8_col_msplit_flat_kernel<2, true>)
-                             : (nsplits <= 64 ? row_to_fp8_col_msplit_flat_kernel<1, false>
-                                              : row_to_fp8_col_msplit_flat_kernel<2, false>);
+      // band walk up to 64 splits on rows of more than 16 bands, else contiguous ranges
+      const bool walk = nsplits <= 64 && bands > 16;
+      auto kernel = narrow_n ? (nsplits > 64 ? row_to_fp8_col_msplit_flat_kernel<2, false, true>
+                                : walk     ? row_to_fp8_col_msplit_flat_kernel<1, true, true>
+                                           : row_to_fp8_col_msplit_flat_kernel<1, false, true>)
+                             : (nsplits > 64 ? row_to_fp8_col_msplit_flat_kernel<2, false, false>
+                                : walk     ? row_to_fp8_col_msplit_flat_kernel<1, true, false>
+                                           : row_to_fp8_col_msplit_flat_kernel<1, false, false>);
       return launch(kernel, grid, dim3(256), reserve, stream, static_cast<const uint8_t*>(q),
                     static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s, lens, offs, soffs, total_rows, N,
                     out_s_rows, eps, out_line, (int)nsplits, (int)tiles_m, (int)bands);
