@@ -664,6 +664,23 @@ def test_row_to_fp8_col_msplit_partial_band(oracle, dev, nsplits, N, seed):
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
+# Up to 64 splits the flat grid hands rows of at most 16 bands (4096
+# columns) out in contiguous ranges and wider ones in band-walk order: both
+# sides of that boundary, whole and partial last bands.
+@pytest.mark.parametrize("nsplits,N,seed", [(8, 4096, 1), (20, 4128, 2), (8, 4352, 3), (64, 4384, 4), (3, 4064, 5)])
+def test_row_to_fp8_col_msplit_order_boundary(oracle, dev, nsplits, N, seed):
+    rng = np.random.default_rng(seed)
+    splits = [int(v) for v in rng.choice([0, 1, 17, 128, 129, 300, 1100], size=nsplits)]
+    if sum(splits) == 0:
+        splits[-1] = 129
+    _say("msplit order boundary", nsplits, N, sum(splits))
+    q, s = payload_from_normal(sum(splits), N, seed)
+    got, got_s = _msplit_sentinel_run(dev, q, s, splits, N)
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(got, eo)
+    np.testing.assert_array_equal(got_s, es.view(np.uint32))
+
+
 # Code rows at an address that is not 16 B aligned take the 128-column
 # kernels (byte-wise code loads); the scales at an odd address too.
 @pytest.mark.parametrize("M,N,shift", [(300, 7168, 4), (128, 384, 8), (1, 64, 1), (700, 2048, 12)])
