@@ -63,8 +63,15 @@ def heavy_tail_weights(M: int, K: int, seed: int, device="cpu", std: float = 0.0
     z = torch.randn((k,), generator=g, device=device)
     chi = torch.randn((k, 3), generator=g, device=device).pow(2).sum(1)
     t3 = z / torch.sqrt(chi / 3.0)
+    # A position drawn more than once takes its last draw, as a sequential
+    # assignment would; a device scatter with repeated indices keeps an
+    # arbitrary one, so repeats are resolved here (stable sort, last of each run).
+    order = torch.argsort(pos, stable=True)
+    ps, ts = pos[order], t3[order]
+    last = torch.ones_like(ps, dtype=torch.bool)
+    last[:-1] = ps[:-1] != ps[1:]
     w = w.view(-1)
-    w[pos] = t3
+    w[ps[last]] = ts[last]
     return (w.view(M, K) * std).to(torch.bfloat16)
 
 

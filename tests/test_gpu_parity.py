@@ -681,6 +681,37 @@ def test_row_to_fp8_col_msplit_order_boundary(oracle, dev, nsplits, N, seed):
     np.testing.assert_array_equal(got_s, es.view(np.uint32))
 
 
+# Widths that are not multiples of 32 (row_bytes = N / 2 any, scales
+# [M, ceil(N / 32)]) take the 128-column tiles with byte-wise code loads.
+@pytest.mark.parametrize("M,N", [(300, 100), (129, 2050), (1, 2), (256, 7166)])
+def test_row_to_fp8_col_odd_width(oracle, dev, M, N):
+    omo = _omo()
+    _say("row_to_fp8_col odd width", M, N)
+    rng = np.random.default_rng(M + N)
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(110, 140, size=(M, (N + 31) // 32)).astype(np.uint8)
+    out = torch.full((N, M), 0xAB, dtype=torch.uint8, device=dev).view(FP8)
+    outs = torch.full(((M + 127) // 128, N), float("nan"), dtype=torch.float32, device=dev)
+    omo.omo_per_token_Mxfp4RowToBf16ToFp8Col(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), out, outs, 1e-10)
+    torch.cuda.synchronize()
+    eo, es = oracle.row_to_fp8_col(q, s)
+    np.testing.assert_array_equal(bits_u8(out), eo)
+    np.testing.assert_array_equal(outs.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
+@pytest.mark.parametrize("splits,N", [([129, 0, 300, 17], 100), ([5] * 70 + [260], 1026)])
+def test_row_to_fp8_col_msplit_odd_width(oracle, dev, splits, N):
+    _say("msplit odd width", len(splits), N)
+    M = sum(splits)
+    rng = np.random.default_rng(M + N)
+    q = rng.integers(0, 256, size=(M, N // 2), dtype=np.uint8)
+    s = rng.integers(110, 140, size=(M, (N + 31) // 32)).astype(np.uint8)
+    got, got_s = _msplit_sentinel_run(dev, q, s, splits, N)
+    eo, es = oracle.row_to_fp8_col_msplit(q, s, splits)
+    np.testing.assert_array_equal(got, eo)
+    np.testing.assert_array_equal(got_s, es.view(np.uint32))
+
+
 # Code rows at an address that is not 16 B aligned take the 128-column
 # kernels (byte-wise code loads); the scales at an odd address too.
 @pytest.mark.parametrize("M,N,shift", [(300, 7168, 4), (128, 384, 8), (1, 64, 1), (700, 2048, 12)])
