@@ -331,6 +331,7 @@ __device__ __forceinline__ int wave_prefix(int v) {
   return v;
 }
 
+template <bool WALK>  // the product's band walk (rows of more than 16 bands), else its contiguous ranges
 __global__ __launch_bounds__(256, 4) void msplit_flat_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                             uint8_t* __restrict__ out, float* __restrict__ out_s,
                                                             const int32_t* __restrict__ lens,
@@ -346,20 +347,36 @@ __global__ __launch_bounds__(256, 4) void msplit_flat_floor(const uint8_t* __res
     start_l = offs[lane];
     sstart_l = soffs[lane];
   }
-  // the product's band walk: split after split, each XCD takes a contiguous
-  // range of ceil(tiles_i / 8) of the split's band-major tiles and walks it
-  // row tile by row tile
-  const int xcd = (int)(blockIdx.x & 7u), j = (int)(blockIdx.x >> 3);
+  // band walk: split after split, each XCD takes a contiguous range of
+  // ceil(tiles_i / 8) of the split's band-major tiles and walks it row tile
+  // by row tile. Ranges: the whole band-major numbering of all splits' tiles
+  // in eight contiguous ranges, one per XCD.
+  const int xcd = (int)(blockIdx.x & 7u);
   const int rows_l = len_l > 0 ? (int)min(((int64_t)len_l + 127) / 128, (int64_t)tm) : 0;
   const int per_l = (rows_l * bands + 7) / 8;
-  const int n_l = min(max(rows_l * bands - xcd * per_l, 0), per_l);
+  const int n_l = WALK ? min(max(rows_l * bands - xcd * per_l, 0), per_l) : rows_l;
   const int incl = wave_prefix(n_l), excl = incl - n_l;
-  if (j >= __builtin_amdgcn_readlane(incl, 63)) return;
-  const uint64_t hit = __ballot(j >= excl && j < incl);
+  int j;
+  if (WALK) {
+    j = (int)(blockIdx.x >> 3);
+    if (j >= __builtin_amdgcn_readlane(incl, 63)) return;
+  } else {
+    const uint32_t n_real = (uint32_t)__builtin_amdgcn_readlane(incl, 63) * (uint32_t)bands;
+    if (blockIdx.x >= n_real) return;
+    j = (int)xcd_order(blockIdx.x, n_real);
+  }
+  const int unit = WALK ? 1 : bands;
+  const uint64_t hit = __ballot(j >= unit * excl && j < unit * incl);
   const int i = (int)__builtin_ctzll(hit);
   const int S = __builtin_amdgcn_readlane(rows_l, i), per = __builtin_amdgcn_readlane(per_l, i);
+  const int r = j - unit * __builtin_amdgcn_readlane(excl, i);
   int tbm, tbn;
-  if (!floor_band_group(xcd, j - __builtin_amdgcn_readlane(excl, i), S, S * bands, per, &tbm, &tbn)) return;
+  if (WALK) {
+    if (!floor_band_group(xcd, r, S, S * bands, per, &tbm, &tbn)) return;
+  } else {
+    tbm = r % S;
+    tbn = r / S;
+  }
   const int64_t bm = tbm, bn = tbn;
   const int64_t len = __builtin_amdgcn_readlane(len_l, i), start = __builtin_amdgcn_readlane(start_l, i),
                 sstart = __builtin_amdgcn_readlane(sstart_l, i);
@@ -549,7 +566,9 @@ __attribute__((visibility("default"))) int omo_floor_rowcol(const void* q, const
 // (residency capped at four workgroups per CU); N % 256 == 0, metadata as the
 // product's (int32 device arrays). Its flat grid reads one split per lane, so
 // it takes at most 64 splits (split x row tile x band beyond): it matches the
-// product's grid only up to 64 splits (the product's flat grid takes 128).
+// product's grid only up to 64 splits (the product's flat grid takes 128),
+// with the product's order (band walk on rows of more than 16 bands, else
+// contiguous ranges).
 __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const void* s, void* out, float* out_s,
                                                             int64_t total_rows, int64_t N, const int32_t* lens,
                                                             const int32_t* offs, const int32_t* soffs, int64_t nsplits,
@@ -562,8 +581,8 @@ __attribute__((visibility("default"))) int omo_floor_msplit(const void* q, const
   const size_t reserve = per_wg > kWideSmemBytes ? (size_t)(per_wg - kWideSmemBytes) : 0;
   const int64_t tm = (max_split_len + 127) / 128, bands = N / 256;
   if (nsplits <= 64 && tm * bands + 7 <= (int64_t)UINT32_MAX / 256 / nsplits) {
-    hipLaunchKernelGGL(msplit_flat_floor, dim3((unsigned)(8 * nsplits * ((tm * bands + 7) / 8))), dim3(256), reserve,
-                       stream,
+    hipLaunchKernelGGL(bands > 16 ? msplit_flat_floor<true> : msplit_flat_floor<false>,
+                       dim3((unsigned)(8 * nsplits * ((tm * bands + 7) / 8))), dim3(256), reserve, stream,
                        static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(s), static_cast<uint8_t*>(out), out_s,
                        lens, offs, soffs, total_rows, N, out_s_rows, (reinterpret_cast<uintptr_t>(out) & 127) == 0,
                        (int)nsplits, (int)tm, (int)bands);
