@@ -452,11 +452,13 @@ struct DualGroup {
 };
 
 // Each XCD takes its band-group share of each item, item after item, over
-// the items' 64-row tiles. cfg5's 24 expert weights (three shapes of 7168 x
-// 2048 / 2048 x 7168, 224 super-tiles each): 208.8 us against 212.3 us for
-// the four-tile kernel over contiguous ranges of all items' super-tiles; on
-// zero-filled buffers 203.7 us against 224.4 us with contiguous ranges of the
-// 64-row tiles and 211.6 us for the four-tile kernel in band groups.
+// the items' 64-row tiles. cfg5's 24 expert weights (16 of 7168 x 2048, 8 of
+// 2048 x 7168, 224 super-tiles each): 208.8 us against 212.3 us for the
+// four-tile kernel over contiguous ranges of all items' super-tiles, 214.4 us
+// with contiguous ranges of all items' 64-row tiles and 223-226 us with whole
+// items per XCD. Smaller items as well: 8 of 2048 x 2048 24.1 against 25.3 us
+// with the contiguous ranges, 16 of 1024 x 4096 43 against 45, 32 of 2048 x
+// 768 35.5-38.4 against 39.6-41.2.
 __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const DualGroup g) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
   __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
