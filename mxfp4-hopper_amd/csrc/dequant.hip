@@ -48,30 +48,39 @@ __device__ __forceinline__ u32x4 dequant_dword_fast(uint32_t c, uint32_t sb) {
   return o;
 }
 
+// Workgroup b covers code dwords [b * 256 * UNROLL, +256 * UNROLL): a
+// workgroup-uniform base pointer per tensor and 32-bit lane offsets, so each
+// load and store takes one address operation.
 template <int UNROLL>
 __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                            u32x4* __restrict__ out, int64_t ndw) {
-  const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
+  constexpr uint32_t kSpan = 256 * UNROLL;
+  const int64_t b0 = (int64_t)blockIdx.x * kSpan;
+  const uint32_t* qb = q + b0;
+  const uint8_t* sb0 = s + (b0 >> 2);
+  u32x4* ob = out + b0;
+  const uint32_t lim = ndw - b0 < (int64_t)kSpan ? (uint32_t)(ndw - b0) : kSpan;  // dwords of this workgroup
   uint32_t c[UNROLL], sb[UNROLL];
+  // Loads at clamped indices, all issued before the first wait: loads under
+  // a per-lane bounds branch made the compiler wait for the first scale byte
+  // at the branch's join before issuing the rest.
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
-    const int64_t i = base + (int64_t)u * 256;
-    if (i < ndw) {
-      c[u] = q[i];
-      sb[u] = s[i >> 2];
-    }
+    const uint32_t i = min(u * 256 + threadIdx.x, lim - 1);
+    c[u] = qb[i];
+    sb[u] = sb0[i >> 2];
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
-    const int64_t i = base + (int64_t)u * 256;
-    if (i >= ndw) continue;
+    const uint32_t i = u * 256 + threadIdx.x;
+    if (i >= lim) continue;
     u32x4 o;
     if (sb[u] - 1u <= 253u) {
       o = dequant_dword_fast(c[u], sb[u]);
     } else {
       o = dequant_dword_ref(c[u], sb[u]);
     }
-    __builtin_nontemporal_store(o, out + i);
+    __builtin_nontemporal_store(o, ob + i);
   }
 }
 
@@ -90,20 +99,18 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
   const uint32_t* qr = reinterpret_cast<const uint32_t*>(q + row * q_stride);
   const uint8_t* sr = s + row * s_stride;
   u32x4* orow = out + row * dpr;
-  const int base = seg * (256 * UNROLL) + (int)threadIdx.x;
+  const uint32_t base = seg * (256 * UNROLL) + threadIdx.x;
   uint32_t c[UNROLL], sb[UNROLL];
 #pragma unroll
-  for (int u = 0; u < UNROLL; u++) {
-    const int i = base + u * 256;
-    if (i < dpr) {
-      c[u] = qr[i];
-      sb[u] = sr[i >> 2];
-    }
+  for (int u = 0; u < UNROLL; u++) {  // clamped, as in dequant_bf16_kernel; unsigned offsets
+    const uint32_t i = min(base + u * 256, (uint32_t)dpr - 1);
+    c[u] = qr[i];
+    sb[u] = sr[i >> 2];
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
-    const int i = base + u * 256;
-    if (i >= dpr) continue;
+    const uint32_t i = base + u * 256;
+    if (i >= (uint32_t)dpr) continue;
     const u32x4 o = (sb[u] - 1u <= 253u) ? dequant_dword_fast(c[u], sb[u]) : dequant_dword_ref(c[u], sb[u]);
     __builtin_nontemporal_store(o, orow + i);
   }

@@ -40,18 +40,34 @@ namespace omo_hip {
 // exponent field: {0x30, 0x38, 0x3C, 0x40, 0x44, 0x48, 0x4C} - 8d. A zero
 // code gives 0 for d <= 0 and the wrapped -inf -> -448 (0xFE) for d >= 1.
 // No NaN pattern arises in this range. The eight bytes form a per-lane
-// table; v_perm_b32 looks up four elements per instruction.
-__device__ __forceinline__ u32x2 to_fp8_dword_fast(uint32_t c, int d) {
-  const uint32_t sh = (uint32_t)(-8 * d);
-  // every byte stays in [0x08, 0x7C], so whole-dword arithmetic is per-byte
-  const uint32_t t_lo = (0x3C383000u + sh * 0x01010100u) | (d >= 1 ? 0xFEu : 0u);
-  const uint32_t t_hi = 0x4C484440u + sh * 0x01010101u;
-  const uint32_t lo = c & 0x0F0F0F0Fu, hi = (c >> 4) & 0x0F0F0F0Fu;
-  const uint32_t a = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // nibbles of elements 0..3
-  const uint32_t b = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // elements 4..7
+// table (t_hi:t_lo); v_perm_b32 looks up four elements per instruction.
+//
+// d = x - 6 with x = max(s) - s_i: the reference's adjust (uint16)(g - s_i)
+// is x - 6 modulo 2^16, and x lies in [0, 255], so d in [-6, 5] is x <= 11.
+__device__ __forceinline__ void fp8_table(uint32_t x, uint32_t& t_lo, uint32_t& t_hi) {
+  // 8x (at most 88) in every byte. With 48 added to each base byte no byte
+  // of the difference borrows, so the dword subtraction is per byte:
+  // byte = base + 48 - 8x = base - 8d.
+  const uint32_t x8 = x << 3;
+  const uint32_t rep = __builtin_amdgcn_perm(x8, x8, 0u);
+  t_hi = 0x7C787470u - rep;
+  const uint32_t lo = 0x6C686058u - rep;  // byte 0 (0x58 - 8x) is replaced below
+  t_lo = __builtin_amdgcn_perm(x >= 7u ? 0xFEu : 0u, lo, 0x03020104u);
+}
+
+// 8 elements of the code dword c under table (t_hi:t_lo). The low and high
+// nibbles of the four code bytes are looked up separately (3-bit magnitude),
+// their sign bits (bits 3 and 7 of each code byte) moved to bit 7 of the
+// looked-up bytes by one bitop3 each (x ^ (y & 0x80808080)), and the two
+// lookups interleaved into element order.
+__device__ __forceinline__ u32x2 to_fp8_dword_fast(uint32_t c, uint32_t t_lo, uint32_t t_hi) {
+  uint32_t lo = __builtin_amdgcn_perm(t_hi, t_lo, c & 0x07070707u);         // elements 0, 2, 4, 6
+  uint32_t hi = __builtin_amdgcn_perm(t_hi, t_lo, (c >> 4) & 0x07070707u);  // elements 1, 3, 5, 7
+  lo = __builtin_amdgcn_bitop3_b32(lo, c << 4, 0x80808080u, 0x78);
+  hi = __builtin_amdgcn_bitop3_b32(hi, c, 0x80808080u, 0x78);
   u32x2 o;
-  o[0] = __builtin_amdgcn_perm(t_hi, t_lo, a & 0x07070707u) ^ ((a << 4) & 0x80808080u);
-  o[1] = __builtin_amdgcn_perm(t_hi, t_lo, b & 0x07070707u) ^ ((b << 4) & 0x80808080u);
+  o[0] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+  o[1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
   return o;
 }
 
@@ -101,7 +117,10 @@ constexpr int kRqRowsSmall = 8;
 // expert-major token order of a MoE permutation); an index outside
 // [0, n_src) reads zero codes and zero scale bytes, i.e. the row a permutation
 // pads with zeros, requantized.
-template <int ROWS, bool ALIGN8>
+// ROWS64: rows addressed with 64-bit products (a gather, or strides or
+// output rows of 2^24 bytes and more); otherwise addresses are a
+// workgroup-uniform tile base plus 32-bit lane offsets (24-bit products).
+template <int ROWS, bool ALIGN8, bool ROWS64>
 __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __restrict__ q, int64_t q_stride,
                                                            const uint8_t* __restrict__ s, int64_t s_stride,
                                                            const int32_t* __restrict__ src, int64_t n_src,
@@ -109,51 +128,88 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
                                                            uint32_t M, uint32_t gpr, uint32_t gx) {
   constexpr int PPR = 8 * kRqGroups;  // pairs per tile row
   constexpr int UNROLL = ROWS * PPR / 256;
+  constexpr int RSTEP = 256 / PPR;    // rows between one lane's pairs
   const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x);
   const uint32_t bx = L % gx, by = L / gx;
-  const int64_t ppr_all = 8 * (int64_t)gpr;
+  const uint32_t t = threadIdx.x;
+  const uint32_t row0 = by * ROWS;                 // first row of the tile
+  const uint32_t cp = bx * PPR + t % PPR;          // the lane's pair column, the same in each of its rows
+  const uint32_t cpc = min(cp, 8 * gpr - 1);
+  const uint32_t lr0 = t / PPR;                    // the lane's first row within the tile
+  // Every load is issued at clamped in-bounds indices (and zeroed afterwards
+  // for a padding row): loads under a per-lane branch made the compiler wait
+  // for each pair's codes at the branch's join before issuing the next
+  // pair's loads, so a lane had one pair in flight instead of all.
+  const uint8_t* qp[UNROLL];
+  const uint8_t* sp[UNROLL];
+  bool pad[UNROLL];
+  if (ROWS64) {
+    int64_t sr[UNROLL];
+    if (src) {
+#pragma unroll
+      for (int u = 0; u < UNROLL; u++) sr[u] = src[min(row0 + lr0 + u * RSTEP, M - 1)];
+    } else {
+#pragma unroll
+      for (int u = 0; u < UNROLL; u++) sr[u] = min(row0 + lr0 + u * RSTEP, M - 1);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; u++) {
+      pad[u] = sr[u] < 0 || sr[u] >= n_src;
+      const int64_t row = pad[u] ? 0 : sr[u];
+      qp[u] = q + row * q_stride + 8 * cpc;
+      sp[u] = s + row * s_stride + 4 * (cpc >> 3);
+    }
+  } else {
+    const uint8_t* qt = q + (int64_t)row0 * q_stride;
+    const uint8_t* st = s + (int64_t)row0 * s_stride;
+#pragma unroll
+    for (int u = 0; u < UNROLL; u++) {
+      const uint32_t lr = min(row0 + lr0 + u * RSTEP, M - 1) - row0;
+      qp[u] = qt + (__umul24(lr, (uint32_t)q_stride) + 8 * cpc);
+      sp[u] = st + (__umul24(lr, (uint32_t)s_stride) + 4 * (cpc >> 3));
+      pad[u] = false;
+    }
+  }
   u32x2 c[UNROLL];
   uint32_t sd[UNROLL];
+  if (n_src > 0) {
 #pragma unroll
-  for (int u = 0; u < UNROLL; u++) {
-    const int e = u * 256 + threadIdx.x;
-    const uint32_t r = by * ROWS + e / PPR, cp = bx * PPR + e % PPR;
-    if (r < M && cp < 8 * gpr) {
-      const int64_t sr = src ? (int64_t)src[r] : (int64_t)r;
-      if (sr >= 0 && sr < n_src) {
-        const uint8_t* p = q + sr * q_stride + 8 * (int64_t)cp;
-        if (ALIGN8) {
-          c[u] = *reinterpret_cast<const u32x2*>(p);
-        } else {
-          c[u][0] = *reinterpret_cast<const uint32_t*>(p);
-          c[u][1] = *reinterpret_cast<const uint32_t*>(p + 4);
-        }
-        sd[u] = *reinterpret_cast<const uint32_t*>(s + sr * s_stride + 4 * (cp >> 3));
+    for (int u = 0; u < UNROLL; u++) {
+      if (ALIGN8) {
+        c[u] = *reinterpret_cast<const u32x2*>(qp[u]);
       } else {
-        c[u][0] = 0u;
-        c[u][1] = 0u;
-        sd[u] = 0u;
+        c[u][0] = *reinterpret_cast<const uint32_t*>(qp[u]);
+        c[u][1] = *reinterpret_cast<const uint32_t*>(qp[u] + 4);
       }
+      sd[u] = *reinterpret_cast<const uint32_t*>(sp[u]);
     }
+  } else {
+#pragma unroll
+    for (int u = 0; u < UNROLL; u++) c[u][0] = c[u][1] = sd[u] = 0u;
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
-    const int e = u * 256 + threadIdx.x;
-    const uint32_t r = by * ROWS + e / PPR, cp = bx * PPR + e % PPR;
-    if (r >= M || cp >= 8 * gpr) continue;
-    const int64_t i = (int64_t)r * ppr_all + cp;
+    if (pad[u]) c[u][0] = c[u][1] = sd[u] = 0u;
+  }
+  const uint32_t sh = 8 * ((t & 7u) >> 1);  // byte of s_i in the group's scale dword (cp & 7 == t & 7)
+  u32x4* ot = out + (int64_t)row0 * (8 * (int64_t)gpr) + bx * PPR;
+  float* os = out_s + (int64_t)(bx * kRqGroups) * M + row0;
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const uint32_t lr = lr0 + u * RSTEP;
+    if (row0 + lr >= M || cp >= 8 * gpr) continue;
     const uint32_t sw = sd[u];
     const uint32_t smax = max(max(sw & 0xFFu, (sw >> 8) & 0xFFu), max((sw >> 16) & 0xFFu, sw >> 24));
-    const uint32_t g16 = (smax - 6u) & 0xFFFFu;
-    const uint32_t s_i = (sw >> (8 * ((cp & 7u) >> 1))) & 0xFFu;
-    const uint32_t adj = (g16 - s_i) & 0xFFFFu;
-    const int d = (int)(adj & 511u) - ((adj & 256u) ? 512 : 0);
+    const uint32_t s_i = (sw >> sh) & 0xFFu;
+    const uint32_t x = smax - s_i;
     u32x2 o0, o1;
-    if ((unsigned)(d + 6) <= 11u) {
-      o0 = to_fp8_dword_fast(c[u][0], d);
-      o1 = to_fp8_dword_fast(c[u][1], d);
+    if (x <= 11u) {
+      uint32_t t_lo, t_hi;
+      fp8_table(x, t_lo, t_hi);
+      o0 = to_fp8_dword_fast(c[u][0], t_lo, t_hi);
+      o1 = to_fp8_dword_fast(c[u][1], t_lo, t_hi);
     } else {
-      const uint32_t offset = (adj << 7) & 0xFFFFu;
+      const uint32_t offset = ((smax - 6u - s_i) << 7) & 0xFFFFu;  // (uint16)(g - s_i) << 7
       o0 = to_fp8_dword_ref(c[u][0], offset);
       o1 = to_fp8_dword_ref(c[u][1], offset);
     }
@@ -162,8 +218,13 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
     o[1] = o0[1];
     o[2] = o1[0];
     o[3] = o1[1];
-    __builtin_nontemporal_store(o, out + i);
-    if ((cp & 7) == 0) out_s[(int64_t)(cp >> 3) * M + r] = __uint_as_float((g16 & 0xFFu) << 23);
+    if (ROWS64) {
+      __builtin_nontemporal_store(o, ot + ((int64_t)lr * (8 * gpr) + t % PPR));
+    } else {
+      const uint32_t ob = (__umul24(lr, 8 * gpr) + t % PPR) * 16u;  // byte offset in the tile, below 2^29
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(ot) + ob));
+    }
+    if ((t & 7u) == 0) os[((t % PPR) >> 3) * M + lr] = __uint_as_float(((smax - 6u) & 0xFFu) << 23);
   }
 }
 
@@ -181,12 +242,21 @@ hipError_t launch_mxfp4_to_fp8_rows(const void* q, int64_t q_stride, const void*
   const int rows = small ? kRqRowsSmall : (src ? kRqRows : kRqRowsPlain);
   const int64_t gy = (M + rows - 1) / rows;
   const bool a8 = (q_stride % 8 == 0) && ((reinterpret_cast<uintptr_t>(q) & 7) == 0);
-  auto kernel = rows == kRqRowsSmall ? (a8 ? mxfp4_to_fp8_kernel<kRqRowsSmall, true> : mxfp4_to_fp8_kernel<kRqRowsSmall, false>)
-                : rows == kRqRowsPlain ? (a8 ? mxfp4_to_fp8_kernel<kRqRowsPlain, true> : mxfp4_to_fp8_kernel<kRqRowsPlain, false>)
-                                       : (a8 ? mxfp4_to_fp8_kernel<kRqRows, true> : mxfp4_to_fp8_kernel<kRqRows, false>);
-  return launch(kernel, dim3((unsigned)(gx * gy)), dim3(256), 0, stream, static_cast<const uint8_t*>(q), q_stride,
-                     static_cast<const uint8_t*>(s), s_stride, src, n_src, static_cast<u32x4*>(out), out_s,
-                     (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
+  const bool r64 = src || q_stride >= (1 << 24) || s_stride >= (1 << 24) || 2 * Kb >= (1 << 24);
+  using Kernel = void (*)(const uint8_t*, int64_t, const uint8_t*, int64_t, const int32_t*, int64_t, u32x4*, float*,
+                          uint32_t, uint32_t, uint32_t);
+  // [rows: 8, 16, 32][a8][r64]
+  static const Kernel table[3][2][2] = {
+      {{mxfp4_to_fp8_kernel<kRqRowsSmall, false, false>, mxfp4_to_fp8_kernel<kRqRowsSmall, false, true>},
+       {mxfp4_to_fp8_kernel<kRqRowsSmall, true, false>, mxfp4_to_fp8_kernel<kRqRowsSmall, true, true>}},
+      {{mxfp4_to_fp8_kernel<kRqRowsPlain, false, false>, mxfp4_to_fp8_kernel<kRqRowsPlain, false, true>},
+       {mxfp4_to_fp8_kernel<kRqRowsPlain, true, false>, mxfp4_to_fp8_kernel<kRqRowsPlain, true, true>}},
+      {{mxfp4_to_fp8_kernel<kRqRows, false, false>, mxfp4_to_fp8_kernel<kRqRows, false, true>},
+       {mxfp4_to_fp8_kernel<kRqRows, true, false>, mxfp4_to_fp8_kernel<kRqRows, true, true>}}};
+  const int ri = rows == kRqRowsSmall ? 0 : rows == kRqRowsPlain ? 1 : 2;
+  return launch(table[ri][a8][r64], dim3((unsigned)(gx * gy)), dim3(256), 0, stream,
+                static_cast<const uint8_t*>(q), q_stride, static_cast<const uint8_t*>(s), s_stride, src, n_src,
+                static_cast<u32x4*>(out), out_s, (uint32_t)M, (uint32_t)gpr, (uint32_t)gx);
 }
 
 hipError_t launch_mxfp4_to_fp8(const void* q, const void* s, void* out, float* out_s, int64_t M, int64_t Kb,

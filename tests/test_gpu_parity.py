@@ -357,6 +357,62 @@ def test_to_fp8_rowwise_cfg4(oracle, dev):
     np.testing.assert_array_equal(outs.view(np.uint32), es.view(np.uint32))
 
 
+def every_gap_payload():
+    """Rows 0..119: block 0 of each 128-group holds scale 255, block b > 0
+    holds 255 - a with a = n % 256 for the group's n-th such block overall,
+    and its 16 code bytes are 16 * ((n // 256) % 16) + 0..15, so every gap
+    max(s) - s_i in 0..255 meets every code byte. Rows 120..127 take group
+    maxima 0..5 (the wrapped g = max(s) - 6) with gaps up to the maximum.
+    Read as (codes [128, 1024], scales [128, 64], pairs seen)."""
+    M, Kb = 128, 1024
+    q = np.zeros((M, Kb), np.uint8)
+    s = np.zeros((M, Kb // 16), np.uint8)
+    seen = set()
+    n = 0
+    for r in range(M):
+        for g in range(Kb // 64):
+            m = 255 if r < 120 else (r * 16 + g) % 6
+            s[r, 4 * g] = m
+            q[r, 64 * g:64 * g + 16] = np.arange(16) * 7
+            for b in range(1, 4):
+                a = n % 256 if r < 120 else n % (m + 1)
+                s[r, 4 * g + b] = m - a
+                lo = 16 * ((n // 256) % 16)
+                q[r, 64 * g + 16 * b:64 * g + 16 * b + 16] = np.arange(lo, lo + 16)
+                if r < 120:
+                    seen.update((a, int(c)) for c in range(lo, lo + 16))
+                n += 1
+    return q, s, seen
+
+
+def test_to_fp8_rowwise_every_gap(oracle, dev):
+    """Every (max(s) - s_i, code byte) pair of the fast path (gaps 0..11) and
+    the restated path (12..255), and group maxima below 6, against the oracle;
+    the plain requant and the gathered one (reversed rows plus padding rows)."""
+    _say("to_fp8 rowwise every gap")
+    q, s, seen = every_gap_payload()
+    assert seen == {(a, c) for a in range(256) for c in range(256)}
+    out, outs = run_to_fp8(q, s, dev)
+    eo, es = oracle.mxfp4_to_fp8(q, s)
+    np.testing.assert_array_equal(out, eo)
+    np.testing.assert_array_equal(outs.view(np.uint32), es.view(np.uint32))
+    omo = _omo()
+    M, Kb = q.shape
+    src = np.concatenate([np.arange(M - 1, -1, -1), [-1, M, -5]]).astype(np.int32)
+    N = src.size
+    gq = np.zeros((N, Kb), np.uint8)
+    gs = np.zeros((N, Kb // 16), np.uint8)
+    gq[:M], gs[:M] = q[::-1], s[::-1]
+    eo2, es2 = oracle.mxfp4_to_fp8(gq, gs)
+    o8 = torch.empty((N, 2 * Kb), dtype=FP8, device=dev)
+    o8s = torch.empty((Kb // 64, N), dtype=torch.float32, device=dev)
+    omo.omo_permute_Mxfp4ToFp8(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev),
+                               torch.from_numpy(src).to(dev), o8, o8s)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits_u8(o8), eo2)
+    np.testing.assert_array_equal(o8s.cpu().numpy().view(np.uint32), es2.view(np.uint32))
+
+
 def test_to_fp8_wrapper_split(oracle, dev):
     from omo_python_api.mxfp4_dequant import omo_per_token_mxfp4ToFp8_wrapper
     _say("to_fp8 wrapper with m_splits")
