@@ -465,7 +465,7 @@ __global__ __launch_bounds__(256) void msplit_band_floor(const uint8_t* __restri
   }
 }
 
-// ---- rowwise FP8 requant, 16 rows x 4 groups of 128 elements (mxfp4_to_fp8_kernel<16, true>)
+// ---- rowwise FP8 requant, 16 rows x 4 groups of 128 elements (mxfp4_to_fp8_kernel<16, true, false>)
 __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                      fu32x4* __restrict__ out, float* __restrict__ out_s, uint32_t M,
                                                      uint32_t gpr, uint32_t gx) {
@@ -494,20 +494,23 @@ __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__
 // ---- dequant to bf16, four code dwords per lane (dequant_bf16_kernel<4>)
 __global__ __launch_bounds__(256) void dequant_floor(const uint32_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                      fu32x4* __restrict__ out, int64_t ndw) {
-  const int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  // the product's addressing: a workgroup base and clamped 32-bit lane offsets
+  const int64_t b0 = (int64_t)blockIdx.x * 1024;
+  const uint32_t* qb = q + b0;
+  const uint8_t* sb0 = s + (b0 >> 2);
+  fu32x4* ob = out + b0;
+  const uint32_t lim = ndw - b0 < 1024 ? (uint32_t)(ndw - b0) : 1024u;
   uint32_t c[4], sb[4];
 #pragma unroll
   for (int u = 0; u < 4; u++) {
-    const int64_t i = base + (int64_t)u * 256;
-    if (i < ndw) {
-      c[u] = q[i];
-      sb[u] = s[i >> 2];
-    }
+    const uint32_t i = min(u * 256 + threadIdx.x, lim - 1);
+    c[u] = qb[i];
+    sb[u] = sb0[i >> 2];
   }
 #pragma unroll
   for (int u = 0; u < 4; u++) {
-    const int64_t i = base + (int64_t)u * 256;
-    if (i < ndw) __builtin_nontemporal_store(fu32x4{c[u], sb[u], c[u] ^ sb[u], c[u] + sb[u]}, out + i);
+    const uint32_t i = u * 256 + threadIdx.x;
+    if (i < lim) __builtin_nontemporal_store(fu32x4{c[u], sb[u], c[u] ^ sb[u], c[u] + sb[u]}, ob + i);
   }
 }
 

@@ -66,10 +66,12 @@ __device__ __forceinline__ uint32_t dpp_quad_xor2(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
 }
 
-// Maximum over the 4 lanes of a quad (all 4 lanes must be active).
+// Maximum over the 4 lanes of a quad (all 4 lanes must be active). With every
+// source lane active, bound_ctrl changes nothing; set, it lets each step fold
+// into one v_max_u32 with a DPP operand.
 __device__ __forceinline__ uint32_t quad_max_u32(uint32_t v) {
-  v = max(v, dpp_quad_xor1(v));
-  v = max(v, dpp_quad_xor2(v));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));
   return v;
 }
 __device__ __forceinline__ float quad_fmax(float v) {
@@ -143,6 +145,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
 // constructor (RNE, satfinite) that the reference uses.
 __device__ __forceinline__ uint32_t fp8x2_from_f32(float a, float b) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
+// Four such floats -> four E4M3 bytes (a in bits 0..7). The first
+// conversion's passed-through upper half is overwritten by the second, so its
+// old operand is a's own bits rather than a register zeroed for it.
+__device__ __forceinline__ uint32_t fp8x4_from_f32(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
 // Workgroup b of a 1-D grid is dispatched to XCD b % 8, and each XCD has its

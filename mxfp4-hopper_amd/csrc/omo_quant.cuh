@@ -53,17 +53,27 @@ __device__ __forceinline__ void quant_chunk_ref(const u32x4& d, float eps, float
   *codes = out;
 }
 
+// Scale of a block whose max |x| bf16 pattern is amax_bits (< 0x7F80):
+// returns y_s = 2^c and sets *byte = c + 127. For amax = (1 + f/128) 2^E,
+// ceil(log2(amax / 6)) = E - 2 + (f > 64) = ((amax_bits + 63) >> 7) - 129, f > 64
+// being the carry of f + 63 into the exponent field. The reference takes the
+// scale of fmaxf(eps, amax) and the scale is monotone in its argument, so c
+// is max(that, c_eps), where c_eps >= -33 already holds the 1e-10 floor:
+// c + 127 = max(((amax_bits + 63) >> 7) - 2, c_eps + 127), and the subtraction
+// inside the shift ((amax_bits - 193) >> 7, arithmetic) only differs below
+// amax_bits = 193, where the maximum takes c_eps + 127 either way.
+__device__ __forceinline__ float fast_block_scale(uint32_t amax_bits, int c_eps, uint32_t* byte) {
+  const int b = max((int)(amax_bits - 193u) >> 7, c_eps + 127);
+  *byte = (uint32_t)b;
+  return __uint_as_float((uint32_t)b << 23);
+}
+
 // Fast path for one chunk: returns the 4 code bytes; *byte gets the scale.
-// amax_bits is the quad-wide max of |x| bit patterns, < 0x7F80.
-__device__ __forceinline__ uint32_t quant_chunk_fast(const u32x4& d, uint32_t amax_bits, float eps, int c_eps,
-                                                     uint32_t* byte) {
-  float xmax = bf16_to_f32(amax_bits);
-  int c = (int)(amax_bits >> 7) - 129 + ((amax_bits & 0x7Fu) > 64u ? 1 : 0);
-  c = c < -33 ? -33 : c;
-  c = (xmax > eps) ? c : c_eps;
-  *byte = (uint32_t)(c + 127);
-  float y_s = exp2i(c);
-  uint32_t r = 0;
+// amax_bits is the quad-wide max of |x| bit patterns, < 0x7F80. The four
+// conversions write the four bytes of r, so its initial value is unused.
+__device__ __forceinline__ uint32_t quant_chunk_fast(const u32x4& d, uint32_t amax_bits, int c_eps, uint32_t* byte) {
+  const float y_s = fast_block_scale(amax_bits, c_eps, byte);
+  uint32_t r = d[0];
   r = cvt_pk_fp4<0>(r, d[0], y_s);
   r = cvt_pk_fp4<1>(r, d[1], y_s);
   r = cvt_pk_fp4<2>(r, d[2], y_s);

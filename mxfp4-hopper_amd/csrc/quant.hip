@@ -18,7 +18,9 @@
 //   * the scale exponent in closed form: for a bf16 amax = (1+f/128)*2^E,
 //     ceil(log2(amax/6)) = E - 2 + (f > 64); amax/6 is either an exact power
 //     of two (f == 64) or at least 0.5% away from one, so rounding of the
-//     quotient never moves the ceiling; the 1e-10 floor is exponent -33;
+//     quotient never moves the ceiling; the scale of fmaxf(eps, amax) is
+//     the larger of the two scales, so eps and the 1e-10 floor (exponent
+//     -33) enter as max(c, c_eps);
 //   * q = x / 2^c is exact and |q| <= 6, so v_cvt_scalef32_pk_fp4_bf16
 //     (round-to-nearest-even, verified bit-exact against the reference rule
 //     over every bf16 value and every reachable c in [-33, 126]) yields the
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(QuantArgs a) {
     if (STANDARD) {
       uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
       if (__builtin_expect(am < 0x7F80u, 1)) {
-        codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
+        codes = quant_chunk_fast(d[u], am, a.c_eps, &byte);
       } else {
         quant_chunk_ref(d[u], a.eps, a.fp4_min, a.fp4_max, &codes, &byte);
       }
@@ -123,7 +125,7 @@ __device__ __forceinline__ void ph_read_phase(const QuantArgs& a, int64_t c0, in
       uint32_t codes, byte;
       const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
       if (__builtin_expect(am < 0x7F80u, 1)) {
-        codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
+        codes = quant_chunk_fast(d[u], am, a.c_eps, &byte);
       } else {
         quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
       }
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantRowsArgs a) {
     uint32_t codes, byte;
     const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
     if (__builtin_expect(am < 0x7F80u, 1)) {
-      codes = quant_chunk_fast(d[u], am, a.eps, a.c_eps, &byte);
+      codes = quant_chunk_fast(d[u], am, a.c_eps, &byte);
     } else {
       quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
     }

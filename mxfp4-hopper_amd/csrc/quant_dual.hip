@@ -40,22 +40,17 @@ constexpr int kDualThreads = 512;
 // Half of a 32-element column block: 8 packed bf16 pairs (rows 2j low, 2j+1
 // high); amax_bits is the whole block's max |x| bit pattern (< 0x7F80).
 // Returns the 8 code bytes.
-__device__ __forceinline__ uint2 quant_half16_fast(const uint32_t (&p)[8], uint32_t amax_bits, float eps, int c_eps,
+__device__ __forceinline__ uint2 quant_half16_fast(const uint32_t (&p)[8], uint32_t amax_bits, int c_eps,
                                                    uint32_t* byte) {
-  const float xmax = bf16_to_f32(amax_bits);
-  int c = (int)(amax_bits >> 7) - 129 + ((amax_bits & 0x7Fu) > 64u ? 1 : 0);
-  c = c < -33 ? -33 : c;
-  c = (xmax > eps) ? c : c_eps;
-  *byte = (uint32_t)(c + 127);
-  const float y_s = exp2i(c);
+  const float y_s = fast_block_scale(amax_bits, c_eps, byte);
   uint2 out;
-  uint32_t r = 0;
+  uint32_t r = p[0];  // all four bytes are written
   r = cvt_pk_fp4<0>(r, p[0], y_s);
   r = cvt_pk_fp4<1>(r, p[1], y_s);
   r = cvt_pk_fp4<2>(r, p[2], y_s);
   r = cvt_pk_fp4<3>(r, p[3], y_s);
   out.x = r;
-  r = 0;
+  r = p[4];
   r = cvt_pk_fp4<0>(r, p[4], y_s);
   r = cvt_pk_fp4<1>(r, p[5], y_s);
   r = cvt_pk_fp4<2>(r, p[6], y_s);
@@ -123,7 +118,7 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
     uint32_t codes, byte;
     const uint32_t am = quad_max_u32(chunk_absmax_bits(d[k]));
     if (__builtin_expect(am < 0x7F80u, 1)) {
-      codes = quant_chunk_fast(d[k], am, eps, c_eps, &byte);
+      codes = quant_chunk_fast(d[k], am, c_eps, &byte);
     } else {
       quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
     }
@@ -169,9 +164,9 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
   amax_b = max(amax_b, dpp_quad_xor1(amax_b));
   uint32_t byte_a, byte_b;
   uint2 qa, qb;
-  if (__builtin_expect(amax_a < 0x7F80u, 1)) qa = quant_half16_fast(ca, amax_a, eps, c_eps, &byte_a);
+  if (__builtin_expect(amax_a < 0x7F80u, 1)) qa = quant_half16_fast(ca, amax_a, c_eps, &byte_a);
   else qa = quant_half16_ref(ca, eps, &byte_a);
-  if (__builtin_expect(amax_b < 0x7F80u, 1)) qb = quant_half16_fast(cb, amax_b, eps, c_eps, &byte_b);
+  if (__builtin_expect(amax_b < 0x7F80u, 1)) qb = quant_half16_fast(cb, amax_b, c_eps, &byte_b);
   else qb = quant_half16_ref(cb, eps, &byte_b);
   const int64_t mo = (m0 + 16 * band) / 2;
   if (active) {
@@ -277,7 +272,7 @@ __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint
       uint32_t codes, byte;
       const uint32_t am = quad_max_u32(chunk_absmax_bits(d[k]));
       if (__builtin_expect(am < 0x7F80u, 1)) {
-        codes = quant_chunk_fast(d[k], am, eps, c_eps, &byte);
+        codes = quant_chunk_fast(d[k], am, c_eps, &byte);
       } else {
         quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
       }
@@ -303,9 +298,9 @@ __device__ __forceinline__ void dual_super4(const uint16_t* __restrict__ x, uint
     amax_b = max(amax_b, dpp_quad_xor1(amax_b));
     uint32_t byte_a, byte_b;
     uint2 qa, qb;
-    if (__builtin_expect(amax_a < 0x7F80u, 1)) qa = quant_half16_fast(ca, amax_a, eps, c_eps, &byte_a);
+    if (__builtin_expect(amax_a < 0x7F80u, 1)) qa = quant_half16_fast(ca, amax_a, c_eps, &byte_a);
     else qa = quant_half16_ref(ca, eps, &byte_a);
-    if (__builtin_expect(amax_b < 0x7F80u, 1)) qb = quant_half16_fast(cb, amax_b, eps, c_eps, &byte_b);
+    if (__builtin_expect(amax_b < 0x7F80u, 1)) qb = quant_half16_fast(cb, amax_b, c_eps, &byte_b);
     else qb = quant_half16_ref(cb, eps, &byte_b);
 #pragma unroll
     for (int s = 0; s < 4; s++) {

@@ -314,8 +314,8 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
           y[k] = v1 * m1;
         }
         // bytes 0, 1 from the low-word convert, bytes 2, 3 from the high-word one
-        w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
-        w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+        w0[j4] = fp8x4_from_f32(x[0], x[1], x[2], x[3]);
+        w1[j4] = fp8x4_from_f32(y[0], y[1], y[2], y[3]);
       }
     } else {
 #pragma unroll
@@ -328,8 +328,8 @@ __device__ __forceinline__ void rc_tile(RowColSmem& sm, int rows_valid, int64_t 
           x[k] = __builtin_amdgcn_fmed3f(v0 * m0, -448.0f, 448.0f);
           y[k] = __builtin_amdgcn_fmed3f(v1 * m1, -448.0f, 448.0f);
         }
-        w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
-        w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+        w0[j4] = fp8x4_from_f32(x[0], x[1], x[2], x[3]);
+        w1[j4] = fp8x4_from_f32(y[0], y[1], y[2], y[3]);
       }
     }
   } else {
@@ -507,8 +507,8 @@ __device__ __forceinline__ void wide_pair_fast(const uint32_t (&cw)[16], const f
       x[k] = CLAMP ? __builtin_amdgcn_fmed3f(v0 * m0, -448.0f, 448.0f) : v0 * m0;
       y[k] = CLAMP ? __builtin_amdgcn_fmed3f(v1 * m1, -448.0f, 448.0f) : v1 * m1;
     }
-    w0[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false), true);
-    w1[j4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+    w0[j4] = fp8x4_from_f32(x[0], x[1], x[2], x[3]);
+    w1[j4] = fp8x4_from_f32(y[0], y[1], y[2], y[3]);
   }
 }
 
@@ -527,11 +527,13 @@ __device__ __forceinline__ void wide_pair_scaled(const uint32_t (&cw)[16], const
     float x[4], y[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) cvt_pk_f32_fp4_once<B>(cw[4 * j4 + k], sc[4 * j4 + k], &x[k], &y[k]);
-    const s16x2 z = {0, 0};
+    // the first conversion's passed-through upper half is overwritten by the second
     const s16x2 a = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(
-        __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(z, x[0], x[1], inv0, false), x[2], x[3], inv0, true);
+        __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(__builtin_bit_cast(s16x2, x[0]), x[0], x[1], inv0, false), x[2], x[3],
+        inv0, true);
     const s16x2 b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(
-        __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(z, y[0], y[1], inv1, false), y[2], y[3], inv1, true);
+        __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(__builtin_bit_cast(s16x2, y[0]), y[0], y[1], inv1, false), y[2], y[3],
+        inv1, true);
     w0[j4] = (uint32_t)(uint16_t)a[0] | ((uint32_t)(uint16_t)a[1] << 16);
     w1[j4] = (uint32_t)(uint16_t)b[0] | ((uint32_t)(uint16_t)b[1] << 16);
   }
@@ -702,13 +704,15 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   // so that the four loads issue back to back: loads under a branch each
   // waited for completion before the next was issued (dense 4000 x 7168:
   // 10.6 against 11.4 us).
+  // Lane t loads chunk t & 7 of rows (t >> 3) + 32k: one 64-bit row product
+  // per lane, the rest workgroup-uniform steps of 32 rows.
   u32x4 cv[4];
+  const uint8_t* qt = q + row0 * (N / 2) + col0 / 2 + 16 * (PARTIAL ? min(t & 7, nch - 1) : (t & 7));
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
-    const int rr = RAGGED ? min(r, rows_valid - 1) : r;
-    const int cc = PARTIAL ? min(c16, nch - 1) : c16;
-    cv[k] = *reinterpret_cast<const u32x4*>(q + (row0 + rr) * (N / 2) + col0 / 2 + cc * 16);
+    const int r = (t >> 3) + 32 * k;
+    const int64_t rr = RAGGED ? min(r, rows_valid - 1) : (t >> 3);
+    cv[k] = *reinterpret_cast<const u32x4*>(qt + rr * (N / 2) + (RAGGED ? 0 : 32 * k * (N / 2)));
   }
   u32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
   if (t < kTile) {
