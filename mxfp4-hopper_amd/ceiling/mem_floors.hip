@@ -491,24 +491,25 @@ __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__
   }
 }
 
-// ---- dequant to bf16, four code dwords per lane (dequant_bf16_kernel<4>)
+// ---- dequant to bf16, U code dwords per lane (dequant_bf16_kernel<U>, the product's choice of U)
+template <int U>
 __global__ __launch_bounds__(256) void dequant_floor(const uint32_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                      fu32x4* __restrict__ out, int64_t ndw) {
   // the product's addressing: a workgroup base and clamped 32-bit lane offsets
-  const int64_t b0 = (int64_t)blockIdx.x * 1024;
+  const int64_t b0 = (int64_t)blockIdx.x * (256 * U);
   const uint32_t* qb = q + b0;
   const uint8_t* sb0 = s + (b0 >> 2);
   fu32x4* ob = out + b0;
-  const uint32_t lim = ndw - b0 < 1024 ? (uint32_t)(ndw - b0) : 1024u;
-  uint32_t c[4], sb[4];
+  const uint32_t lim = ndw - b0 < 256 * U ? (uint32_t)(ndw - b0) : 256u * U;
+  uint32_t c[U], sb[U];
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
+  for (int u = 0; u < U; u++) {
     const uint32_t i = min(u * 256 + threadIdx.x, lim - 1);
     c[u] = qb[i];
     sb[u] = sb0[i >> 2];
   }
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
+  for (int u = 0; u < U; u++) {
     const uint32_t i = u * 256 + threadIdx.x;
     if (i < lim) __builtin_nontemporal_store(fu32x4{c[u], sb[u], c[u] ^ sb[u], c[u] + sb[u]}, ob + i);
   }
@@ -640,8 +641,16 @@ __attribute__((visibility("default"))) int omo_floor_requant(const void* q, cons
 __attribute__((visibility("default"))) int omo_floor_dequant(const void* q, const void* s, void* out, int64_t ndw,
                                                              hipStream_t stream) {
   if (ndw <= 0) return -1;
-  hipLaunchKernelGGL(dequant_floor, dim3((unsigned)((ndw + 1023) / 1024)), dim3(256), 0, stream,
-                     static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<fu32x4*>(out), ndw);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return -1;
+  if ((ndw + 1023) / 1024 <= 8 * (int64_t)cus)  // the product's rule
+    hipLaunchKernelGGL(dequant_floor<4>, dim3((unsigned)((ndw + 1023) / 1024)), dim3(256), 0, stream,
+                       static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<fu32x4*>(out), ndw);
+  else
+    hipLaunchKernelGGL(dequant_floor<2>, dim3((unsigned)((ndw + 511) / 512)), dim3(256), 0, stream,
+                       static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<fu32x4*>(out), ndw);
   return (int)hipGetLastError();
 }
 

@@ -129,10 +129,18 @@ hipError_t launch_dequant_rows(const void* q, int64_t q_stride, const void* s, i
 hipError_t launch_dequant_bf16(const void* q, const void* s, void* out, int64_t nbytes, hipStream_t stream) {
   const int64_t ndw = nbytes / 4;
   if (ndw == 0) return hipSuccess;
-  constexpr int U = 4;
-  const int64_t blocks = (ndw + 256 * U - 1) / (256 * U);
-  return launch((dequant_bf16_kernel<U>), dim3((unsigned)blocks), dim3(256), 0, stream,
-                     static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<u32x4*>(out), ndw);
+  // Four dwords per lane when the launch is one round of resident
+  // workgroups (8 per CU): every load is then issued at once (cfg1's 4096 x
+  // 4096 takes 1.4 us longer as two rounds of two-dword workgroups). Larger
+  // tensors take two dwords per lane, more rounds with less tail each:
+  // 8192 x 7168 21.6 against 22.0 us, 4096 x 7168 11.5 against 11.6 us.
+  const int64_t b4 = (ndw + 1023) / 1024;
+  if (b4 <= 8 * (int64_t)current_device_caps().cus)
+    return launch((dequant_bf16_kernel<4>), dim3((unsigned)b4), dim3(256), 0, stream,
+                  static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<u32x4*>(out), ndw);
+  const int64_t b2 = (ndw + 511) / 512;
+  return launch((dequant_bf16_kernel<2>), dim3((unsigned)b2), dim3(256), 0, stream, static_cast<const uint32_t*>(q),
+                static_cast<const uint8_t*>(s), static_cast<u32x4*>(out), ndw);
 }
 
 }  // namespace omo_hip
