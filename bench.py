@@ -277,7 +277,10 @@ def floors_leg(torch, args, dev, cur, lib, _abi, wl):
                                                    "ranges per XCD"),
                              (4, "dual_m_fastest_ranges", "the product's stores in contiguous M-fastest super-tile "
                                                           "ranges per XCD (each XCD finishing a band before the "
-                                                          "next)")):
+                                                          "next)"),
+                             (5, "dual_aligned_groups", "the product's stores with each XCD owning whole 8-band "
+                                                        "groups (64 B halves of the row-scale lines) and an eighth "
+                                                        "of the leftover groups")):
         alt(name, f"dual-layout floor 7168x18432: {what}", wl.dual_quant_bytes(n), 2,
             lambda i, kind=kind: chk(fl.omo_floor_dual_variant(kind, xd[i].data_ptr(), od[i][0].data_ptr(),
                                                                od[i][1].data_ptr(), od[i][2].data_ptr(),

@@ -64,6 +64,26 @@ __device__ __forceinline__ bool floor_band_group(int xcd, int j, int S, int T, i
   return true;
 }
 
+// Aligned groups (bands % 8 == 0): bands in groups of 8, i.e. one 64 B half of
+// every row-scale line, so no half is written by two XCDs. With G = bands / 8
+// groups, XCD x takes the whole groups x, x + 8, ... (the first 8 (G / 8)),
+// walked super-row by super-row, then its eighth of the last G % 8 groups,
+// numbered super-row by super-row. False past the XCD's share.
+__device__ __forceinline__ bool floor_aligned_groups(int xcd, int j, int S, int bands, int* ms, int* kb) {
+  const int G = bands / 8, q = G / 8, r = G % 8;
+  if (j < 8 * q * S) {
+    const int w = j % (8 * q);
+    *ms = j / (8 * q);
+    *kb = 8 * (xcd + 8 * (w / 8)) + w % 8;
+    return true;
+  }
+  if (j >= 8 * q * S + r * S) return false;
+  const int i = xcd * r * S + (j - 8 * q * S);
+  *ms = i / (8 * r);
+  *kb = 64 * q + i % (8 * r);
+  return true;
+}
+
 // M % 256 == 0, K % 256 == 0, 16 B aligned buffers (the shapes the bench uses).
 // SCM 0: the product's scale stores (8 B per row per tile, 8 B per column per
 // super-tile, ordinary stores); SCM 1: no scale stores (the bound the code
@@ -73,7 +93,8 @@ __device__ __forceinline__ bool floor_band_group(int xcd, int j, int S, int T, i
 // layout, the bound a layout-free scale store would set. ORDER 0: the
 // product's band-group order; 1: contiguous ranges of the M-fastest
 // numbering per XCD (each XCD finishing one band before the next); 2:
-// contiguous ranges of the K-fastest numbering.
+// contiguous ranges of the K-fastest numbering; 3: aligned groups
+// (floor_aligned_groups).
 template <int SCM, int ORDER>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void dual_floor(
     const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q, uint8_t* __restrict__ row_s,
@@ -86,6 +107,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void d
   int ms, kb, logical;
   if (ORDER == 0) {
     if (!floor_band_group(b % 8, b / 8, tiles_ms, tiles, per_xcd, &ms, &kb)) return;
+    logical = kb * tiles_ms + ms;
+  } else if (ORDER == 3) {
+    if (!floor_aligned_groups(b % 8, b / 8, tiles_ms, tiles_k, &ms, &kb)) return;
     logical = kb * tiles_ms + ms;
   } else {
     logical = (b % 8) * per_xcd + b / 8;
@@ -542,13 +566,18 @@ __attribute__((visibility("default"))) int omo_floor_dual(const void* x, void* r
 // Other schedules of the dual-layout traffic on the same buffers: kind 1 =
 // no scale stores, 2 = scales as whole non-temporal lines (layout-free
 // bound), 3 = the product's stores in contiguous K-fastest ranges per XCD,
-// 4 = in contiguous M-fastest ranges per XCD.
+// 4 = in contiguous M-fastest ranges per XCD, 5 = in aligned groups (K % 2048 == 0).
 __attribute__((visibility("default"))) int omo_floor_dual_variant(int kind, const void* x, void* row_q, void* row_s,
                                                                   void* col_q, void* col_s, int64_t M, int64_t K,
                                                                   hipStream_t stream) {
-  if (M <= 0 || K <= 0 || M % 256 || K % 256 || kind < 1 || kind > 4) return -1;
+  if (M <= 0 || K <= 0 || M % 256 || K % 256 || kind < 1 || kind > 5) return -1;
+  if (kind == 5 && K % 2048) return -1;
   const int tiles_ms = (int)(M / 256), tiles = (int)(tiles_ms * (K / 256)), per_xcd = (tiles + 7) / 8;
-  auto kern = kind == 1 ? dual_floor<1, 0> : kind == 2 ? dual_floor<2, 0> : kind == 3 ? dual_floor<0, 2> : dual_floor<0, 1>;
+  auto kern = kind == 1 ? dual_floor<1, 0>
+              : kind == 2 ? dual_floor<2, 0>
+              : kind == 3 ? dual_floor<0, 2>
+              : kind == 4 ? dual_floor<0, 1>
+                          : dual_floor<0, 3>;
   hipLaunchKernelGGL(kern, dim3((unsigned)(per_xcd * 8)), dim3(512), 0, stream, static_cast<const uint16_t*>(x),
                      static_cast<uint32_t*>(row_q), static_cast<uint8_t*>(row_s), static_cast<uint8_t*>(col_q),
                      static_cast<uint8_t*>(col_s), M, K, tiles_ms, tiles, per_xcd);

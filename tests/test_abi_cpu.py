@@ -187,8 +187,10 @@ def test_bench_floor_library_exports_and_shape_checks():
     assert lib.omo_floor_dequant(None, None, None, 0, None) == -1
     lib.omo_floor_dual_variant.argtypes = [ctypes.c_int, P, P, P, P, P, I64, I64, P]
     lib.omo_floor_msplit_band.argtypes = [P, P, P, P, I64, P, P, P, I64, I64, P]
-    assert lib.omo_floor_dual_variant(0, None, None, None, None, None, 7168, 18432, None) == -1  # kinds 1..4
-    assert lib.omo_floor_dual_variant(5, None, None, None, None, None, 7168, 18432, None) == -1
+    assert lib.omo_floor_dual_variant(0, None, None, None, None, None, 7168, 18432, None) == -1  # kinds 1..5
+    assert lib.omo_floor_dual_variant(6, None, None, None, None, None, 7168, 18432, None) == -1
+    # aligned groups need whole 8-band groups
+    assert lib.omo_floor_dual_variant(5, None, None, None, None, None, 7168, 18432 + 256, None) == -1
     assert lib.omo_floor_dual_variant(1, None, None, None, None, None, 7168 + 64, 18432, None) == -1
     # the band schedule holds a whole split's band in LDS: longer splits and N % 64 are refused
     assert lib.omo_floor_msplit_band(None, None, None, None, 7168, None, None, None, 8, 4353, None) == -1
