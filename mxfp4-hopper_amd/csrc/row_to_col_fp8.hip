@@ -463,6 +463,7 @@ struct WideSmem {
   uint8_t codes[kTile * kWidePitch];
   uint32_t fscales[8][kTile];  // s << 23, [MX column of the tile][row]
   uint8_t scales[8][kTile];
+  uint32_t odd_scales[2];      // per staging wave: a scale byte of its rows outside [1, 252]
 };
 
 // The output pass converts with volatile asm, so the compiler neither keeps
@@ -543,14 +544,14 @@ __device__ __forceinline__ void wide_pair_scaled(const uint32_t (&cw)[16], const
 // 8cg .. 8cg+7 of tile rows 16qq .. 16qq+15 and hands column e's 16 bytes
 // (rows in order) to put(e, w). codes: the tile's first LDS code row (rows
 // permuted by lds_row, pitch bytes apart); scl / fscl: the 128 scale bytes
-// and 2^(s-127) patterns of the lane's MX column. The scale-row entry of
+// and 2^(s-127) patterns of the lane's MX column; fast: every scale byte of
+// the tile is in [1, 252] (else the restatement). The scale-row entry of
 // column 8cg + qq goes to out_s_lane when store_s. The 8 lanes of a code
 // dword must be 8 adjacent lanes of a wave.
 template <bool MSPLIT, typename Put>
 __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, const uint8_t* scl, const uint32_t* fscl,
-                                             int cg, int qq, float eps, bool store_s, float* __restrict__ out_s_lane,
-                                             Put&& put) {
-  const u32x4 sw = *reinterpret_cast<const u32x4*>(scl + 16 * qq);
+                                             int cg, int qq, float eps, bool fast, bool store_s,
+                                             float* __restrict__ out_s_lane, Put&& put) {
   uint32_t cw[16];
   float sc[16];
 #pragma unroll
@@ -561,7 +562,6 @@ __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, co
   }
 #pragma unroll
   for (int j = 0; j < 16; j++) cw[j] = *reinterpret_cast<const uint32_t*>(codes + lds_row(16 * qq + j) * pitch + 4 * cg);
-  const bool fast = bytes_in_1_252(sw[0]) && bytes_in_1_252(sw[1]) && bytes_in_1_252(sw[2]) && bytes_in_1_252(sw[3]);
   float a[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) a[e] = MSPLIT ? 0.0f : eps;
@@ -571,6 +571,7 @@ __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, co
     wide_amax_fast<2>(cw, sc, a);
     wide_amax_fast<3>(cw, sc, a);
   } else {
+    const u32x4 sw = *reinterpret_cast<const u32x4*>(scl + 16 * qq);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       const float s16 = bf16_to_f32(((sw[j >> 2] >> (8 * (j & 3))) & 0xFFu) << 7);
@@ -655,6 +656,7 @@ __device__ __forceinline__ void wide_convert(const uint8_t* codes, int pitch, co
       put(7, w1);
     }
   } else {
+    const u32x4 sw = *reinterpret_cast<const u32x4*>(scl + 16 * qq);
 #pragma unroll 1
     for (int e = 0; e < 8; e++) {
       uint32_t w[4] = {0u, 0u, 0u, 0u};
@@ -746,12 +748,18 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
       sm.scales[c][t] = (uint8_t)b;
       sm.fscales[c][t] = b << 23;
     }
+    // the fast path's test, once per tile: every scale byte in [1, 252]
+    // (padding rows and missing columns hold 127); the two staging waves
+    // each record whether any of their rows fails it
+    const int odd = __any(!(bytes_in_1_252(sv[0]) && bytes_in_1_252(sv[1])));
+    if ((t & 63) == 0) sm.odd_scales[t >> 6] = (uint32_t)odd;
   }
   __syncthreads();
+  const bool fast = (sm.odd_scales[0] | sm.odd_scales[1]) == 0u;
   const int qq = t & 7, cg = t >> 3, mx = cg >> 2;
   const bool col_ok = !PARTIAL || mx < nch;  // this lane's 8 element columns exist
   uint8_t* o = obase + 8 * cg * cstride + 16 * qq;
-  wide_convert<MSPLIT>(sm.codes, kWidePitch, sm.scales[mx], sm.fscales[mx], cg, qq, eps, col_ok,
+  wide_convert<MSPLIT>(sm.codes, kWidePitch, sm.scales[mx], sm.fscales[mx], cg, qq, eps, fast, col_ok,
                        out_s_row + 8 * cg + qq, [&](int e, const u32x4& w) {
                          if (PARTIAL && !col_ok) return;
                          if (RAGGED && !line_nt) rc_store(o + e * cstride, w, 16 * qq, rows_valid);

@@ -1101,6 +1101,30 @@ def test_permute_rows_byte_pieces(dev):
         np.testing.assert_array_equal(bits_u8(a), b)
 
 
+def test_permute_without_source_rows(oracle, dev):
+    """Zero source rows (no token routed anywhere, an empty code tensor): every
+    output row is a padding row, so the gather writes zero rows and the fused
+    requant writes the requant of zero codes and zero scale bytes; neither
+    reads the empty inputs."""
+    omo = _omo()
+    _say("permute with no source rows")
+    H, N = 7168, 37
+    codes = torch.empty((0, H // 2), dtype=torch.uint8, device=dev)
+    scales = torch.empty((0, H // 32), dtype=torch.uint8, device=dev)
+    src = torch.full((N,), -1, dtype=torch.int32, device=dev)
+    oq = torch.full((N, H // 2), 0xAB, dtype=torch.uint8, device=dev)
+    osc = torch.full((N, H // 32), 0xCD, dtype=torch.uint8, device=dev)
+    omo.omo_mxfp4_permute_rows(codes, scales, src, oq, osc)
+    o8 = torch.empty((N, H), dtype=FP8, device=dev)
+    o8s = torch.empty((H // 128, N), dtype=torch.float32, device=dev)
+    omo.omo_permute_Mxfp4ToFp8(codes, scales, src, o8, o8s)
+    torch.cuda.synchronize()
+    assert not bool(oq.any()) and not bool(osc.any())
+    eo, es = oracle.mxfp4_to_fp8(np.zeros((N, H // 2), np.uint8), np.zeros((N, H // 32), np.uint8))
+    np.testing.assert_array_equal(bits_u8(o8), eo)
+    np.testing.assert_array_equal(o8s.cpu().numpy().view(np.uint32), es.view(np.uint32))
+
+
 @pytest.mark.parametrize("T,H,E,k,pad,seed", [(300, 7168, 8, 2, 0, 1), (64, 256, 4, 1, 7, 2), (5, 128, 3, 3, 0, 3),
                                               (40, 1024, 16, 0, 3, 4)])
 def test_permute_rows_and_fp8(oracle, dev, T, H, E, k, pad, seed):
