@@ -88,7 +88,9 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __res
 // s + r * s_stride (bytes), output [rows, K] bf16 contiguous. Reads the
 // expert-parallel payload row [codes | scales] in place instead of the two
 // .contiguous() copies of its unpacking (code/megatron-0.15.0rc7.diff:101-122).
-// Workgroup b covers segment b % bpr of row b / bpr.
+// Workgroup b covers segment b % bpr of row b / bpr. Four dwords per lane
+// at any launch size: at 4096 x 7168 (896 dwords per row) two per lane,
+// with half the second segment idle, took 12.4 against 11.5 us.
 template <int UNROLL>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ q, int64_t q_stride,
                                                            const uint8_t* __restrict__ s, int64_t s_stride,

@@ -205,7 +205,9 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
 // Memory-only copies of this schedule (the same loads and stores, no
 // arithmetic) run within 1-2 us of the kernel: its time is set by the mix of
 // the strided 512 B row reads with the 128 B code lines and the 8-byte scale
-// pieces, whose lines other workgroups complete.
+// pieces, whose lines other workgroups complete. Rowwise codes leave
+// non-temporally and the column lines through L2: temporal row codes ran
+// the same, non-temporal column lines 79 against 75-78 us.
 constexpr int kSuperSteps = 4;
 constexpr int kSuperRows = kDualRows * kSuperSteps;  // 256
 
@@ -453,7 +455,10 @@ struct DualGroup {
 // with contiguous ranges of all items' 64-row tiles and 223-226 us with whole
 // items per XCD. Smaller items as well: 8 of 2048 x 2048 24.1 against 25.3 us
 // with the contiguous ranges, 16 of 1024 x 4096 43 against 45, 32 of 2048 x
-// 768 35.5-38.4 against 39.6-41.2.
+// 768 35.5-38.4 against 39.6-41.2. Each XCD a run of row tiles of each item
+// (all its bands, so the items of 8 bands write whole row-scale halves from
+// one XCD) took 215-218 us for those items and 224-226 us for all items,
+// against 206-211 us.
 __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const DualGroup g) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
   __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];

@@ -795,6 +795,9 @@ __global__ __launch_bounds__(256, 4) void row_to_fp8_col_wide_kernel(const uint8
                                                                      float* __restrict__ out_s, int64_t M, int64_t N,
                                                                      float eps) {
   __shared__ WideSmem sm;
+  // bands fastest within each XCD's contiguous range (each XCD a run of row
+  // tiles, every band): 4096 x 7168 8.9 us against 9.3 with row tiles
+  // fastest and 9.2-9.4 with each XCD a 2-D block of tiles
   const uint32_t L = xcd_contiguous(blockIdx.x, gridDim.x), gx = (uint32_t)((N + kWideCols - 1) / kWideCols);
   const int64_t bn = L % gx, bm = L / gx;
   const int64_t row0 = bm * kTile, col0 = bn * kWideCols;
