@@ -95,48 +95,64 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(QuantArgs a) {
 // each): loads two steps ahead 24.4 against 23.2 us; steps of 1024 or 4096
 // chunks 25.9 / 24.0; writing the first half of the round while the second
 // is read 27.0 against 23.7; step i of every workgroup in one contiguous
-// region (workgroups interleaved) 23.7 against 23.0.
+// region (workgroups interleaved) 23.7 against 23.0; temporal code stores in
+// the write phase 24.1 against 23.6 (and no faster 4096 x 4096 round trip).
 constexpr int kPhThreads = 1024;
 constexpr int kPhUnroll = 2;
+
+// Quantizes the step of chunks [i0, i0 + kPhThreads * kPhUnroll) held in d
+// (lane t: chunks i0 + u * kPhThreads + t) into lds_q / lds_s, skipping
+// chunks at or past n.
+__device__ __forceinline__ void ph_convert_step(const QuantArgs& a, const u32x4 (&d)[kPhUnroll], int i0, int n,
+                                                uint32_t* lds_q, uint8_t* lds_s) {
+  const int t = threadIdx.x;
+  const bool quad_leader = (t & 3) == 0;
+#pragma unroll
+  for (int u = 0; u < kPhUnroll; u++) {
+    const int i = i0 + u * kPhThreads + t;
+    if (i >= n) continue;
+    uint32_t codes, byte;
+    const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
+    if (__builtin_expect(am < 0x7F80u, 1)) {
+      codes = quant_chunk_fast(d[u], am, a.c_eps, &byte);
+    } else {
+      quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
+    }
+    lds_q[i] = codes;
+    if (quad_leader) lds_s[i >> 2] = (uint8_t)byte;
+  }
+}
 
 // Read phase of the two-phase kernels: loads chunks [c0, c0 + n) of a.x (n a
 // multiple of 4, so quads are whole), quantizes them and leaves the code
 // dwords in lds_q[0, n) and the scale bytes in lds_s[0, n / 4). The caller
-// synchronizes before reading them.
+// synchronizes before reading them. Each step's loads are issued before the
+// previous step is converted; the last step is peeled off so that it issues
+// no loads past the share (a reload of chunk 0 per lane there, unused, cost
+// 23.43 against 23.12 us at 8192 x 7168 and 16.15 against 15.90 us for the
+// 4096 x 4096 quantize + dequantize round trip).
 __device__ __forceinline__ void ph_read_phase(const QuantArgs& a, int64_t c0, int n, uint32_t* lds_q, uint8_t* lds_s) {
   const int t = threadIdx.x;
-  const bool quad_leader = (t & 3) == 0;
+  constexpr int kStep = kPhThreads * kPhUnroll;
   u32x4 nx[kPhUnroll];
 #pragma unroll
   for (int u = 0; u < kPhUnroll; u++) {
     const int i = u * kPhThreads + t;
     nx[u] = __builtin_nontemporal_load(a.x + c0 + (i < n ? i : 0));
   }
-  for (int i0 = 0; i0 < n; i0 += kPhThreads * kPhUnroll) {
+  int i0 = 0;
+  for (; i0 + kStep < n; i0 += kStep) {
     u32x4 d[kPhUnroll];
 #pragma unroll
     for (int u = 0; u < kPhUnroll; u++) d[u] = nx[u];
-    // the next step's loads (past the end: a reload of chunk 0, unused)
 #pragma unroll
     for (int u = 0; u < kPhUnroll; u++) {
-      const int i = i0 + kPhThreads * kPhUnroll + u * kPhThreads + t;
+      const int i = i0 + kStep + u * kPhThreads + t;
       nx[u] = __builtin_nontemporal_load(a.x + c0 + (i < n ? i : 0));
     }
-#pragma unroll
-    for (int u = 0; u < kPhUnroll; u++) {
-      const int i = i0 + u * kPhThreads + t;
-      if (i >= n) continue;
-      uint32_t codes, byte;
-      const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
-      if (__builtin_expect(am < 0x7F80u, 1)) {
-        codes = quant_chunk_fast(d[u], am, a.c_eps, &byte);
-      } else {
-        quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
-      }
-      lds_q[i] = codes;
-      if (quad_leader) lds_s[i >> 2] = (uint8_t)byte;
-    }
+    ph_convert_step(a, d, i0, n, lds_q, lds_s);
   }
+  ph_convert_step(a, nx, i0, n, lds_q, lds_s);
 }
 
 __global__ __launch_bounds__(kPhThreads) void quant_phased_kernel(QuantArgs a, int64_t share, int round) {
@@ -319,7 +335,8 @@ hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, 
   // 6-8% slower two-phase than quant_rowwise_kernel, both in 9 / 17 steps and
   // with the surplus chunks loaded alongside the first step (8 / 16 steps);
   // several rounds per workgroup (alternating read and write phases) measured
-  // 6-12% slower.
+  // 6-12% slower, and 4096 x 4096 as one round of one-pass workgroups (four
+  // chunks per lane) 0.8 us slower per quantize + dequantize round trip.
   const int64_t share = ((a.nchunks + dc.cus - 1) / dc.cus + 63) / 64 * 64;
   const int64_t cap = (int64_t)dc.lds_per_workgroup * 4 / 17 / 64 * 64;
   const int64_t steps = (share + kPhThreads * kPhUnroll - 1) / (kPhThreads * kPhUnroll);

@@ -458,7 +458,8 @@ struct DualGroup {
 // 768 35.5-38.4 against 39.6-41.2. Each XCD a run of row tiles of each item
 // (all its bands, so the items of 8 bands write whole row-scale halves from
 // one XCD) took 215-218 us for those items and 224-226 us for all items,
-// against 206-211 us.
+// against 206-211 us. The four-tile kernel in this per-item band-group order
+// (quant_dual_grouped_super_kernel) made the cfg5 layer step 3.5 us slower.
 __global__ __launch_bounds__(kDualThreads) void quant_dual_grouped_kernel(const DualGroup g) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kDualRows * kDualPitch];
   __shared__ __attribute__((aligned(8))) uint8_t rs_tile[kDualRows * 8];
