@@ -46,38 +46,60 @@ struct QuantArgs {
   int c_eps;                    // scale exponent when amax == eps (fast path)
 };
 
-template <int UNROLL, bool STANDARD>
+// EAGER: every chunk of the lane is loaded (at a clamped index), converted
+// and only then stored, so no wait separates one chunk's stores from the
+// next chunk's conversion. Otherwise each chunk is loaded under a bounds
+// test and stored before the next one converts; the wait for its loads
+// before the second chunk then also covers the first chunk's stores (loads
+// and stores share one counter), which slows each wave down. That pacing
+// pays on tensors too large for one LDS round per CU (16431 x 7168: 46.6
+// against 47.4 us eager) and costs elsewhere (16431 x 2048 15.45 against
+// 15.03 us, 2048 x 2048 3.53 against 3.37, 1000 x 7168 4.72 against 4.48;
+// 16431 x 4096 27.8 either way).
+template <int UNROLL, bool STANDARD, bool EAGER>
 __global__ __launch_bounds__(256) void quant_rowwise_kernel(QuantArgs a) {
   const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
+  const bool quad_leader = (threadIdx.x & 3u) == 0u;
   u32x4 d[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int64_t ch = base + (int64_t)u * 256;
-    if (ch < a.nchunks) d[u] = __builtin_nontemporal_load(a.x + ch);
+    if (EAGER) d[u] = __builtin_nontemporal_load(a.x + (ch < a.nchunks ? ch : a.nchunks - 1));
+    else if (ch < a.nchunks) d[u] = __builtin_nontemporal_load(a.x + ch);
   }
-  const bool quad_leader = (threadIdx.x & 3u) == 0u;
+  uint32_t codes[UNROLL], byte[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int64_t ch = base + (int64_t)u * 256;
     // nchunks is a multiple of 4 and quads are 4-aligned, so a quad is
-    // either fully inside or fully outside the tensor.
-    if (ch >= a.nchunks) continue;
-    uint32_t codes, byte;
+    // either fully inside or fully outside the tensor (EAGER: an outside
+    // quad converts four copies of the last chunk and stores nothing).
+    if (!EAGER && ch >= a.nchunks) continue;
     if (STANDARD) {
       uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
       if (__builtin_expect(am < 0x7F80u, 1)) {
-        codes = quant_chunk_fast(d[u], am, a.c_eps, &byte);
+        codes[u] = quant_chunk_fast(d[u], am, a.c_eps, &byte[u]);
       } else {
-        quant_chunk_ref(d[u], a.eps, a.fp4_min, a.fp4_max, &codes, &byte);
+        quant_chunk_ref(d[u], a.eps, a.fp4_min, a.fp4_max, &codes[u], &byte[u]);
       }
     } else {
-      quant_chunk_ref(d[u], a.eps, a.fp4_min, a.fp4_max, &codes, &byte);
+      quant_chunk_ref(d[u], a.eps, a.fp4_min, a.fp4_max, &codes[u], &byte[u]);
     }
+    if (EAGER) continue;
     // Codes are streamed out non-temporally (each wave store is 256
     // contiguous bytes); the one-byte scale stores stay temporal, which
     // measured faster for them.
-    __builtin_nontemporal_store(codes, a.q + ch);
-    if (quad_leader) a.s[ch >> 2] = (uint8_t)byte;
+    __builtin_nontemporal_store(codes[u], a.q + ch);
+    if (quad_leader) a.s[ch >> 2] = (uint8_t)byte[u];
+  }
+  if (EAGER) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; u++) {
+      const int64_t ch = base + (int64_t)u * 256;
+      if (ch >= a.nchunks) continue;
+      __builtin_nontemporal_store(codes[u], a.q + ch);
+      if (quad_leader) a.s[ch >> 2] = (uint8_t)byte[u];
+    }
   }
 }
 
@@ -346,7 +368,10 @@ hipError_t launch_quant_rowwise(const void* x, void* q, void* s, int64_t numel, 
     return launch(quant_phased_kernel, dim3((unsigned)dc.cus), dim3(kPhThreads), (size_t)round * 4 + round / 4,
                        stream, a, share, round);
   }
-  auto kernel = standard ? quant_rowwise_kernel<U, true> : quant_rowwise_kernel<U, false>;
+  // per-chunk stores where the share exceeds one LDS round (see quant_rowwise_kernel)
+  const bool eager = share <= cap;
+  auto kernel = standard ? (eager ? quant_rowwise_kernel<U, true, true> : quant_rowwise_kernel<U, true, false>)
+                         : (eager ? quant_rowwise_kernel<U, false, true> : quant_rowwise_kernel<U, false, false>);
   return launch(kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 
