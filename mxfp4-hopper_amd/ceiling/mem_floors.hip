@@ -161,6 +161,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void d
 // ---- grouped dual-layout quantize, one 64 x 256 tile per workgroup (quant_dual_grouped_kernel)
 constexpr int kFloorGroupMax = 32;
 
+// Forms every value of v here, in code every lane runs, so that the waits
+// for their loads come before the stores that follow (a value formed inside
+// a store's bounds test left the compiler a wait at the test's join that
+// covered the earlier stores too), as the product kernels' conversions do.
+template <int N>
+__device__ __forceinline__ void floor_materialize(fu32x4 (&v)[N]) {
+#pragma unroll
+  for (int u = 0; u < N; u++) asm volatile("" : "+v"(v[u]));
+}
+
 struct FloorItem {
   const uint16_t* x;
   uint32_t* row_q;
@@ -177,10 +187,10 @@ struct FloorGroup {
 };
 
 // One tile's loads and stores as the product's one-tile kernel issues them
-// (M % 64 == 0, K % 256 == 0): four 16 B non-temporal loads per lane, 4 B
-// non-temporal row-code stores, 64 rows' 8 scale bytes gathered in LDS and
-// stored after the barrier, then per column pair two 8 B code stores and a
-// 2-byte scale store (SCM 1: no scale stores).
+// (M % 64 == 0, K % 256 == 0): four 16 B non-temporal loads per lane, then
+// four 4 B non-temporal row-code stores, 64 rows' 8 scale bytes gathered in
+// LDS and stored after the barrier, then per column pair two 8 B code stores
+// and a 2-byte scale store (SCM 1: no scale stores).
 template <int SCM>
 __device__ __forceinline__ void dual_tile_floor(const FloorItem& it, int64_t m0, int64_t k0, uint8_t* tile,
                                                 uint8_t* rs_tile) {
@@ -195,9 +205,11 @@ __device__ __forceinline__ void dual_tile_floor(const FloorItem& it, int64_t m0,
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     *reinterpret_cast<fu32x4*>(tile + (r0 + 16 * k) * 512 + ((cc ^ (k << 2)) * 16)) = d[k];
-    __builtin_nontemporal_store(d[k].x ^ d[k].y, rq + k * 2 * K);
     if ((t & 3) == 0) rs_tile[(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)d[k].z;
   }
+  floor_materialize(d);
+#pragma unroll
+  for (int k = 0; k < 4; k++) __builtin_nontemporal_store(d[k].x ^ d[k].y, rq + k * 2 * K);
   __syncthreads();
   if (SCM == 0 && t < 64)
     *reinterpret_cast<fu32x2*>(it.row_s + (m0 + t) * (K / 32) + k0 / 32) = *reinterpret_cast<const fu32x2*>(rs_tile + t * 8);
@@ -505,13 +517,18 @@ __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__
     c[u] = *reinterpret_cast<const fu32x2*>(q + rr * kb + 8 * (int64_t)cpc);
     sd[u] = *reinterpret_cast<const uint32_t*>(s + rr * (kb / 16) + 4 * (cpc >> 3));
   }
+  // every store after both pairs' loads, as the product orders them
+  fu32x4 v[2];
+#pragma unroll
+  for (int u = 0; u < 2; u++) v[u] = fu32x4{c[u][0], c[u][1], sd[u], c[u][0] ^ sd[u]};
+  floor_materialize(v);
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const int e = u * 256 + threadIdx.x;
     const uint32_t r = by * 16 + e / 32, cp = bx * 32 + e % 32;
     if (r >= M || cp >= 8 * gpr) continue;
-    __builtin_nontemporal_store(fu32x4{c[u][0], c[u][1], sd[u], c[u][0] ^ sd[u]}, out + (int64_t)r * ppr + cp);
-    if ((cp & 7) == 0) out_s[(int64_t)(cp >> 3) * M + r] = __uint_as_float(sd[u] & 0x3FFFFFFFu);
+    __builtin_nontemporal_store(v[u], out + (int64_t)r * ppr + cp);
+    if ((cp & 7) == 0) out_s[(int64_t)(cp >> 3) * M + r] = __uint_as_float(v[u][2] & 0x3FFFFFFFu);
   }
 }
 
@@ -532,10 +549,14 @@ __global__ __launch_bounds__(256) void dequant_floor(const uint32_t* __restrict_
     c[u] = qb[i];
     sb[u] = sb0[i >> 2];
   }
+  fu32x4 v[U];  // every store after all loads, as the product orders them
+#pragma unroll
+  for (int u = 0; u < U; u++) v[u] = fu32x4{c[u], sb[u], c[u] ^ sb[u], c[u] + sb[u]};
+  floor_materialize(v);
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const uint32_t i = u * 256 + threadIdx.x;
-    if (i < lim) __builtin_nontemporal_store(fu32x4{c[u], sb[u], c[u] ^ sb[u], c[u] + sb[u]}, ob + i);
+    if (i < lim) __builtin_nontemporal_store(v[u], ob + i);
   }
 }
 

@@ -70,17 +70,22 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __res
     c[u] = qb[i];
     sb[u] = sb0[i >> 2];
   }
+  // All outputs are formed before the first store: a store ahead of the
+  // next dword's conversion made the wait for that dword's loads wait for
+  // the store as well (loads and stores share one counter).
+  u32x4 o[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    if (sb[u] - 1u <= 253u) {
+      o[u] = dequant_dword_fast(c[u], sb[u]);
+    } else {
+      o[u] = dequant_dword_ref(c[u], sb[u]);
+    }
+  }
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const uint32_t i = u * 256 + threadIdx.x;
-    if (i >= lim) continue;
-    u32x4 o;
-    if (sb[u] - 1u <= 253u) {
-      o = dequant_dword_fast(c[u], sb[u]);
-    } else {
-      o = dequant_dword_ref(c[u], sb[u]);
-    }
-    __builtin_nontemporal_store(o, ob + i);
+    if (i < lim) __builtin_nontemporal_store(o[u], ob + i);
   }
 }
 
@@ -109,12 +114,14 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
     c[u] = qr[i];
     sb[u] = sr[i >> 2];
   }
+  u32x4 o[UNROLL];  // all outputs before the first store, as in dequant_bf16_kernel
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++)
+    o[u] = (sb[u] - 1u <= 253u) ? dequant_dword_fast(c[u], sb[u]) : dequant_dword_ref(c[u], sb[u]);
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const uint32_t i = base + u * 256;
-    if (i >= (uint32_t)dpr) continue;
-    const u32x4 o = (sb[u] - 1u <= 253u) ? dequant_dword_fast(c[u], sb[u]) : dequant_dword_ref(c[u], sb[u]);
-    __builtin_nontemporal_store(o, orow + i);
+    if (i < (uint32_t)dpr) __builtin_nontemporal_store(o[u], orow + i);
   }
 }
 

@@ -229,26 +229,32 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantRowsArgs a) {
   uint32_t* qr = reinterpret_cast<uint32_t*>(a.q + row * a.q_stride);
   uint8_t* sr = a.s + row * a.s_stride;
   const int base = seg * (256 * UNROLL) + (int)threadIdx.x;
+  // loads at clamped indices and stores after every conversion, as in the
+  // EAGER form of quant_rowwise_kernel (quads past the row convert copies
+  // of its last chunk and store nothing)
   u32x4 d[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int c = base + u * 256;
-    if (c < cpr) d[u] = __builtin_nontemporal_load(xr + c);
+    d[u] = __builtin_nontemporal_load(xr + (c < cpr ? c : cpr - 1));
   }
   const bool quad_leader = (threadIdx.x & 3u) == 0u;
+  uint32_t codes[UNROLL], byte[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
+    if (__builtin_expect(am < 0x7F80u, 1)) {
+      codes[u] = quant_chunk_fast(d[u], am, a.c_eps, &byte[u]);
+    } else {
+      quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes[u], &byte[u]);
+    }
+  }
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const int c = base + u * 256;
     if (c >= cpr) continue;  // whole quads
-    uint32_t codes, byte;
-    const uint32_t am = quad_max_u32(chunk_absmax_bits(d[u]));
-    if (__builtin_expect(am < 0x7F80u, 1)) {
-      codes = quant_chunk_fast(d[u], am, a.c_eps, &byte);
-    } else {
-      quant_chunk_ref(d[u], a.eps, -6.0f, 6.0f, &codes, &byte);
-    }
-    __builtin_nontemporal_store(codes, qr + c);
-    if (quad_leader) sr[c >> 2] = (uint8_t)byte;
+    __builtin_nontemporal_store(codes[u], qr + c);
+    if (quad_leader) sr[c >> 2] = (uint8_t)byte[u];
   }
 }
 

@@ -110,22 +110,28 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
   }
   const bool quad_leader = (t & 3) == 0;
   uint32_t* rq = row_q + (m0 + r0) * (K / 8) + col / 8;
+  uint32_t codes[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     // row r0 + 16k is in 16-row band k: its chunks are stored XORed by 4k,
     // so the four bands sit in four different 64 B bank ranges
     *reinterpret_cast<u32x4*>(tile + (r0 + 16 * k) * kDualPitch + ((cc ^ (k << 2)) * 16)) = d[k];
-    uint32_t codes, byte;
+    uint32_t byte;
     const uint32_t am = quad_max_u32(chunk_absmax_bits(d[k]));
     if (__builtin_expect(am < 0x7F80u, 1)) {
-      codes = quant_chunk_fast(d[k], am, c_eps, &byte);
+      codes[k] = quant_chunk_fast(d[k], am, c_eps, &byte);
     } else {
-      quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes, &byte);
+      quant_chunk_ref(d[k], eps, -6.0f, 6.0f, &codes[k], &byte);
     }
-    if (r0 + 16 * k < rows_valid && col < K) __builtin_nontemporal_store(codes, rq + k * 2 * K);  // 16 rows down
     // the 8 scale bytes of a tile row are gathered in LDS and leave as one store
     if (quad_leader) rs_tile[(r0 + 16 * k) * 8 + (cc >> 2)] = (uint8_t)byte;
   }
+  // The code stores follow all four conversions: a store under the bounds
+  // test ahead of the next chunk made the wait for that chunk's load wait
+  // for the store as well (loads and stores share one counter).
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+    if (r0 + 16 * k < rows_valid && col < K) __builtin_nontemporal_store(codes[k], rq + k * 2 * K);  // 16 rows down
   __syncthreads();
   if (t < rows_valid) {
     uint8_t* rs = row_s + (m0 + t) * (K / 32) + k0 / 32;

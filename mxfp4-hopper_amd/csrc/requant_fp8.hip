@@ -194,10 +194,13 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
   const uint32_t sh = 8 * ((t & 7u) >> 1);  // byte of s_i in the group's scale dword (cp & 7 == t & 7)
   u32x4* ot = out + (int64_t)row0 * (8 * (int64_t)gpr) + bx * PPR;
   float* os = out_s + (int64_t)(bx * kRqGroups) * M + row0;
+  // Every pair is converted before the first store: a store ahead of the
+  // next pair's conversion made the wait for that pair's loads wait for the
+  // store as well (loads and stores share one counter).
+  u32x4 ov[UNROLL];
+  uint32_t gs[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
-    const uint32_t lr = lr0 + u * RSTEP;
-    if (row0 + lr >= M || cp >= 8 * gpr) continue;
     const uint32_t sw = sd[u];
     const uint32_t smax = max(max(sw & 0xFFu, (sw >> 8) & 0xFFu), max((sw >> 16) & 0xFFu, sw >> 24));
     const uint32_t s_i = (sw >> sh) & 0xFFu;
@@ -213,18 +216,23 @@ __global__ __launch_bounds__(256) void mxfp4_to_fp8_kernel(const uint8_t* __rest
       o0 = to_fp8_dword_ref(c[u][0], offset);
       o1 = to_fp8_dword_ref(c[u][1], offset);
     }
-    u32x4 o;
-    o[0] = o0[0];
-    o[1] = o0[1];
-    o[2] = o1[0];
-    o[3] = o1[1];
+    ov[u][0] = o0[0];
+    ov[u][1] = o0[1];
+    ov[u][2] = o1[0];
+    ov[u][3] = o1[1];
+    gs[u] = ((smax - 6u) & 0xFFu) << 23;
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; u++) {
+    const uint32_t lr = lr0 + u * RSTEP;
+    if (row0 + lr >= M || cp >= 8 * gpr) continue;
     if (ROWS64) {
-      __builtin_nontemporal_store(o, ot + ((int64_t)lr * (8 * gpr) + t % PPR));
+      __builtin_nontemporal_store(ov[u], ot + ((int64_t)lr * (8 * gpr) + t % PPR));
     } else {
       const uint32_t ob = (__umul24(lr, 8 * gpr) + t % PPR) * 16u;  // byte offset in the tile, below 2^29
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(ot) + ob));
+      __builtin_nontemporal_store(ov[u], reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(ot) + ob));
     }
-    if ((t & 7u) == 0) os[((t % PPR) >> 3) * M + lr] = __uint_as_float(((smax - 6u) & 0xFFu) << 23);
+    if ((t & 7u) == 0) os[((t % PPR) >> 3) * M + lr] = __uint_as_float(gs[u]);
   }
 }
 
