@@ -483,6 +483,11 @@ __device__ __forceinline__ void cvt_pk_f32_fp4_once(uint32_t src, float scale, f
   *hi = r[1];
 }
 
+// Column maxima of the lane's 16 rows in fp32, two values per conversion.
+// Measured and not kept: sign bits cleared and v_cvt_scalef32_pk_bf16_fp4
+// into packed 16-bit maxima (two columns per v_pk_max_u16, exact for scale
+// bytes 1..252, a quarter fewer instructions): 9.17 against 8.86 us at
+// 4096 x 7168.
 template <int B>
 __device__ __forceinline__ void wide_amax_fast(const uint32_t (&cw)[16], const float (&sc)[16], float (&a)[8]) {
 #pragma unroll
