@@ -396,7 +396,10 @@ __device__ __forceinline__ bool band_group_tile(int xcd, int j, int S, int T, in
 
 // At most 80 VGPRs (six waves per SIMD): three 512-thread workgroups per CU,
 // which the LDS (52 KB each) also allows; at 86 the compiler's own choice,
-// two fit and the kernel ran 8% slower.
+// two fit and the kernel ran 8% slower. Loading the next tile into the
+// registers the row pass has consumed, before the column pass, needs 95
+// (two workgroups per CU: 72.75 against 72.0 us at cfg3); within 80 even a
+// one-chunk prefetch spills.
 __global__ __launch_bounds__(kDualThreads) __attribute__((amdgpu_waves_per_eu(6))) void quant_dual_super_kernel(
     const uint16_t* __restrict__ x, uint32_t* __restrict__ row_q, uint8_t* __restrict__ row_s,
     uint8_t* __restrict__ col_q, uint8_t* __restrict__ col_s, int64_t M, int64_t K, int tiles_ms, int tiles,
