@@ -98,7 +98,9 @@ __device__ __forceinline__ u32x2 to_fp8_dword_ref(uint32_t c, uint32_t offset) {
 // [K/128, M]: a whole 128 B line with 32-row tiles, half of one with 16-row
 // tiles, whose other half comes from the next row tile, placed on the same
 // XCD by the contiguous renumbering below, so no line is assembled from
-// partial writes on different XCDs. FP8 bytes are written non-temporally; codes are read with ordinary
+// partial writes on different XCDs. FP8 bytes are written non-temporally
+// (the fp32 scales, 64 B pieces of lines, ordinarily: non-temporal they
+// took 4096 x 7168 from 7.8 to 9.4 us); codes are read with ordinary
 // loads (non-temporal code loads made this kernel and the transposed one
 // 15-16% slower). The tile height (ROWS) is 16 rows without a gather and 32
 // with one (the launcher says why); inputs of few rows take 8-row tiles, so
