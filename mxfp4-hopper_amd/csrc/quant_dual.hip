@@ -213,7 +213,8 @@ __device__ __forceinline__ void dual_tile(const uint16_t* __restrict__ x, uint32
 // the strided 512 B row reads with the 128 B code lines and the 8-byte scale
 // pieces, whose lines other workgroups complete. Rowwise codes leave
 // non-temporally and the column lines through L2: temporal row codes ran
-// the same, non-temporal column lines 79 against 75-78 us.
+// the same, non-temporal column lines 79 against 75-78 us (and, in the
+// band-group order, 76.5 against 71.7 us).
 constexpr int kSuperSteps = 4;
 constexpr int kSuperRows = kDualRows * kSuperSteps;  // 256
 
