@@ -532,7 +532,7 @@ __global__ __launch_bounds__(256) void requant_floor(const uint8_t* __restrict__
   }
 }
 
-// ---- dequant to bf16, U code dwords per lane (dequant_bf16_kernel<U>, the product's choice of U)
+// ---- dequant to bf16, U code dwords per lane (dequant_bf16_kernel<U, U == 4>, the product's choice of U)
 template <int U>
 __global__ __launch_bounds__(256) void dequant_floor(const uint32_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                      fu32x4* __restrict__ out, int64_t ndw) {
@@ -546,7 +546,7 @@ __global__ __launch_bounds__(256) void dequant_floor(const uint32_t* __restrict_
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const uint32_t i = min(u * 256 + threadIdx.x, lim - 1);
-    c[u] = qb[i];
+    c[u] = U == 4 ? __builtin_nontemporal_load(qb + i) : qb[i];  // the product's load policy
     sb[u] = sb0[i >> 2];
   }
   fu32x4 v[U];  // every store after all loads, as the product orders them

@@ -50,8 +50,9 @@ __device__ __forceinline__ u32x4 dequant_dword_fast(uint32_t c, uint32_t sb) {
 
 // Workgroup b covers code dwords [b * 256 * UNROLL, +256 * UNROLL): a
 // workgroup-uniform base pointer per tensor and 32-bit lane offsets, so each
-// load and store takes one address operation.
-template <int UNROLL>
+// load and store takes one address operation. NT_CODES: code dwords are
+// loaded non-temporally (scale bytes, each read by four lanes, never).
+template <int UNROLL, bool NT_CODES>
 __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __restrict__ q, const uint8_t* __restrict__ s,
                                                            u32x4* __restrict__ out, int64_t ndw) {
   constexpr uint32_t kSpan = 256 * UNROLL;
@@ -67,7 +68,7 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const uint32_t* __res
 #pragma unroll
   for (int u = 0; u < UNROLL; u++) {
     const uint32_t i = min(u * 256 + threadIdx.x, lim - 1);
-    c[u] = qb[i];
+    c[u] = NT_CODES ? __builtin_nontemporal_load(qb + i) : qb[i];
     sb[u] = sb0[i >> 2];
   }
   // All outputs are formed before the first store: a store ahead of the
@@ -143,13 +144,17 @@ hipError_t launch_dequant_bf16(const void* q, const void* s, void* out, int64_t 
   // 4096 takes 1.4 us longer as two rounds of two-dword workgroups). Larger
   // tensors take two dwords per lane, more rounds with less tail each:
   // 8192 x 7168 21.6 against 22.0 us, 4096 x 7168 11.5 against 11.6 us.
+  // Code loads are non-temporal in the one-round launch only: 4096 x 4096
+  // 7.14 against 7.20 us from cold buffers and the quantize + dequantize
+  // round trip 15.14 against 15.66 us, while 8192 x 7168 in rounds took
+  // 24.7 against 21.6 us that way.
   const int64_t b4 = (ndw + 1023) / 1024;
   if (b4 <= 8 * (int64_t)current_device_caps().cus)
-    return launch((dequant_bf16_kernel<4>), dim3((unsigned)b4), dim3(256), 0, stream,
+    return launch((dequant_bf16_kernel<4, true>), dim3((unsigned)b4), dim3(256), 0, stream,
                   static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<u32x4*>(out), ndw);
   const int64_t b2 = (ndw + 511) / 512;
-  return launch((dequant_bf16_kernel<2>), dim3((unsigned)b2), dim3(256), 0, stream, static_cast<const uint32_t*>(q),
-                static_cast<const uint8_t*>(s), static_cast<u32x4*>(out), ndw);
+  return launch((dequant_bf16_kernel<2, false>), dim3((unsigned)b2), dim3(256), 0, stream,
+                static_cast<const uint32_t*>(q), static_cast<const uint8_t*>(s), static_cast<u32x4*>(out), ndw);
 }
 
 }  // namespace omo_hip
