@@ -296,7 +296,8 @@ __device__ __forceinline__ void wide_floor_tile(uint8_t* sm, const uint8_t* __re
   for (int k = 0; k < 4; k++) {
     const int id = t + 256 * k, r = id >> 3, c16 = id & 7;
     const int rr = RAGGED ? min(r, rows_valid - 1) : r;
-    cv[k] = *reinterpret_cast<const fu32x4*>(q + (row0 + rr) * (N / 2) + col0 / 2 + c16 * 16);
+    const fu32x4* src = reinterpret_cast<const fu32x4*>(q + (row0 + rr) * (N / 2) + col0 / 2 + c16 * 16);
+    cv[k] = RAGGED ? __builtin_nontemporal_load(src) : *src;  // per split non-temporal, as the product
   }
   fu32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
   if (t < 128) sv = *reinterpret_cast<const fu32x2*>(s + (row0 + (RAGGED ? min(t, rows_valid - 1) : t)) * (N / 32) + col0 / 32);

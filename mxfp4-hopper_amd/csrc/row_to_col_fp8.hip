@@ -712,14 +712,18 @@ __device__ __forceinline__ void wide_tile(WideSmem& sm, const uint8_t* __restric
   // waited for completion before the next was issued (dense 4000 x 7168:
   // 10.6 against 11.4 us).
   // Lane t loads chunk t & 7 of rows (t >> 3) + 32k: one 64-bit row product
-  // per lane, the rest workgroup-uniform steps of 32 rows.
+  // per lane, the rest workgroup-uniform steps of 32 rows. Per split the code
+  // loads are non-temporal (cfg5's 8 splits 50.3 against 49.0 us); the
+  // dense kernel, one round of resident workgroups, keeps ordinary ones
+  // (4096 x 7168 8.9 against 9.5 us non-temporal).
   u32x4 cv[4];
   const uint8_t* qt = q + row0 * (N / 2) + col0 / 2 + 16 * (PARTIAL ? min(t & 7, nch - 1) : (t & 7));
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int r = (t >> 3) + 32 * k;
     const int64_t rr = RAGGED ? min(r, rows_valid - 1) : (t >> 3);
-    cv[k] = *reinterpret_cast<const u32x4*>(qt + rr * (N / 2) + (RAGGED ? 0 : 32 * k * (N / 2)));
+    const u32x4* src = reinterpret_cast<const u32x4*>(qt + rr * (N / 2) + (RAGGED ? 0 : 32 * k * (N / 2)));
+    cv[k] = MSPLIT ? __builtin_nontemporal_load(src) : *src;
   }
   u32x2 sv = {0x7F7F7F7Fu, 0x7F7F7F7Fu};
   if (t < kTile) {
